@@ -1,0 +1,314 @@
+// FP -> SC-code quantizers for gfx950.
+//
+// One pipeline covers the six quantizer variants of the reference (fused per-row /
+// per-tensor / per-head Triton kernels and the torch row-group quantizers):
+//   1. reduce   : one wavefront per (row, column segment) reduces max|x| or (min, max)
+//                 and folds it into its (row group, segment) statistic with an atomic max
+//                 on an order-preserving integer key (max/min are exact, so the result is
+//                 independent of reduction order);
+//   2. finalize : one thread per (group, segment) derives scale / reciprocal / zero-point
+//                 with the variant's fp32 (or float64 host-style) operation order;
+//   3. quantize : one wavefront per row writes the GEMM code bytes (zero-padded to the
+//                 GEMM's row/column padding), the reference API outputs and row sums.
+// All three are HBM-bound streaming passes (the second input read mostly hits L2/MALL).
+#include "common.h"
+
+namespace scmp {
+
+struct QParams {
+    float s, inv, zp, pad;
+    double s64, zp64;
+};
+
+__device__ __forceinline__ uint32_t key_of(float f) {
+    uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float float_of_key(uint32_t k) {
+    uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(b);
+}
+
+__device__ __forceinline__ float load_x(const scmp_quant_args &a, int64_t r, int64_t c) {
+    float v = a.x[r * a.ld + c];
+    if (a.smooth_mode == SCMP_SMOOTH_DIV) v = __fdiv_rn(v, a.smooth[c]);
+    else if (a.smooth_mode == SCMP_SMOOTH_MUL) v = __fmul_rn(v, a.smooth[c]);
+    return v;
+}
+
+__device__ __forceinline__ bool is_asym(int variant) {
+    return variant == SCMP_Q_GROUP_ASYM || variant == SCMP_Q_TENSOR_ASYM;
+}
+
+__global__ void stats_init_kernel(uint32_t *stats, int64_t n) {
+    int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i < n) stats[i] = 0u;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// stats[unit*2 + 0] = key(max) or bits(max|x|); stats[unit*2 + 1] = key(-min)
+__global__ void reduce_kernel(scmp_quant_args a, int64_t group, int64_t segw, int64_t nseg,
+                              uint32_t *stats) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    const int64_t ntask = a.rows * nseg;
+    const bool asym = is_asym(a.variant);
+    for (int64_t task = wave; task < ntask; task += nwaves) {
+        int64_t r = task / nseg, sgi = task - r * nseg;
+        int64_t c0 = sgi * segw, c1 = c0 + segw < a.cols ? c0 + segw : a.cols;
+        float mx = -INFINITY, mn = INFINITY, am = 0.0f;
+        for (int64_t c = c0 + lane; c < c1; c += 64) {
+            float v = load_x(a, r, c);
+            if (asym) {
+                mx = fmaxf(mx, v);
+                mn = fminf(mn, v);
+            } else {
+                am = fmaxf(am, fabsf(v));
+            }
+        }
+        int64_t unit = (r / group) * nseg + sgi;
+        if (asym) {
+            mx = wave_max(mx);
+            mn = wave_min(mn);
+            if (lane == 0) {
+                atomicMax(&stats[unit * 2 + 0], key_of(mx));
+                atomicMax(&stats[unit * 2 + 1], key_of(-mn));
+            }
+        } else {
+            am = wave_max(am);
+            if (lane == 0) atomicMax(&stats[unit * 2 + 0], __float_as_uint(am));
+        }
+    }
+}
+
+__global__ void finalize_kernel(scmp_quant_args a, int64_t nunits, const uint32_t *stats,
+                                QParams *prm) {
+    int64_t u = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (u >= nunits) return;
+    const float eps = 1e-5f;
+    const float qf = (float)a.q_max;
+    QParams p = {0.f, 0.f, 0.f, 0.f, 0.0, 0.0};
+    switch (a.variant) {
+    case SCMP_Q_GROUP_SYM:
+    case SCMP_Q_ROW_SYM:
+    case SCMP_Q_HEAD_SYM: {
+        // max(|x|) clamped at 1e-5f; scale = A / Q; inv = 1 / scale (fused kernels,
+        // quant/fused.py:76-79; per-head host math kernels.py:490-495; grouped
+        // quant/grouped.py:46-47)
+        float A = fmax_first(__uint_as_float(stats[u * 2]), eps);
+        p.s = __fdiv_rn(A, qf);
+        p.inv = __fdiv_rn(1.0f, p.s);
+        p.s64 = (double)p.s;
+        break;
+    }
+    case SCMP_Q_TENSOR_SYM: {
+        // Python floats: max(|max|, |min|, 1e-5) / q_max; 1.0 / scale -> fp32 kernel arg
+        // (sc/kernels.py:1173-1174, quant/fused.py:172-174)
+        double A = (double)__uint_as_float(stats[u * 2]);
+        A = A > 1e-5 ? A : 1e-5;
+        p.s64 = __ddiv_rn(A, (double)a.q_max);
+        p.inv = (float)__ddiv_rn(1.0, p.s64);
+        p.s = (float)p.s64;
+        break;
+    }
+    case SCMP_Q_GROUP_ASYM: {
+        // quant/grouped.py:111-115
+        float mx = float_of_key(stats[u * 2]);
+        float mn = -float_of_key(stats[u * 2 + 1]);
+        float range = fmax_first(__fsub_rn(mx, mn), eps);
+        p.s = __fdiv_rn(range, qf);
+        float z = rne(__fdiv_rn(-mn, p.s));
+        p.zp = fmin_first(fmax_first(z, 0.0f), qf);
+        p.inv = __fdiv_rn(1.0f, p.s);
+        p.s64 = (double)p.s;
+        p.zp64 = (double)p.zp;
+        break;
+    }
+    case SCMP_Q_TENSOR_ASYM: {
+        // quant/fused.py:204-209 in Python floats
+        double mx = (double)float_of_key(stats[u * 2]);
+        double mn = -(double)float_of_key(stats[u * 2 + 1]);
+        double range = mx - mn;
+        range = range > 1e-5 ? range : 1e-5;
+        p.s64 = __ddiv_rn(range, (double)a.q_max);
+        p.inv = (float)__ddiv_rn(1.0, p.s64);
+        double z = __builtin_rint(__ddiv_rn(-mn, p.s64));
+        z = z < 0.0 ? 0.0 : (z > (double)a.q_max ? (double)a.q_max : z);
+        p.zp64 = z;
+        p.zp = (float)z;
+        p.s = (float)p.s64;
+        break;
+    }
+    }
+    prm[u] = p;
+}
+
+__global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, int64_t nseg,
+                                const QParams *prm) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    const int64_t nrows_total = a.code && a.code_rows > a.rows ? a.code_rows : a.rows;
+    const float qf = (float)a.q_max;
+    const bool asym = is_asym(a.variant);
+    const float qlo = asym ? 0.0f : (a.variant == SCMP_Q_HEAD_SYM ? -(qf + 1.0f) : -qf);
+    const float rq = __fdiv_rn((float)a.rng_levels, qf);
+    const float rf = (float)a.rng_levels;
+    for (int64_t r = wave; r < nrows_total; r += nwaves) {
+        if (r >= a.rows) {                       // zero code rows of the GEMM padding
+            for (int64_t c = lane; c < a.code_ld; c += 64) a.code[r * a.code_ld + c] = 0;
+            continue;
+        }
+        const int64_t g = r / group;
+        float rsum = 0.0f;
+        for (int64_t c = lane; c < a.cols; c += 64) {
+            const int64_t sgi = c / segw;
+            const QParams p = prm[g * nseg + sgi];
+            float v = load_x(a, r, c);
+            float t;
+            switch (a.variant) {
+            case SCMP_Q_GROUP_SYM: t = __fdiv_rn(v, p.s); break;
+            case SCMP_Q_GROUP_ASYM: t = __fadd_rn(__fdiv_rn(v, p.s), p.zp); break;
+            case SCMP_Q_TENSOR_ASYM: t = __fadd_rn(__fmul_rn(v, p.inv), p.zp); break;
+            default: t = __fmul_rn(v, p.inv); break;
+            }
+            float q = fmin_first(fmax_first(rne(t), qlo), qf);
+            float mag = fabsf(q);
+            const int64_t o = r * a.out_ld + c;
+            if (a.beta16 || a.beta32) {
+                float bf = a.beta_formula == 0 ? __fmul_rn(mag, rq)
+                                               : __fdiv_rn(__fmul_rn(mag, rf), qf);
+                int bv = (int)rne(bf);
+                if (a.beta16) a.beta16[o] = (int16_t)bv;
+                if (a.beta32) a.beta32[o] = bv;
+            }
+            if (a.sign) {
+                int8_t sg;
+                if (a.variant == SCMP_Q_GROUP_SYM) sg = q < 0.0f ? -1 : 1;
+                else sg = q > 0.0f ? 1 : (q < 0.0f ? -1 : 0);
+                a.sign[o] = sg;
+            }
+            if (a.xint) a.xint[o] = q;
+            if (a.code) {
+                int qi = (int)q;
+                uint8_t code;
+                if (a.code_kind == SCMP_CODE_Q) {
+                    code = (uint8_t)(qi & 0xff);
+                } else {
+                    int cls = a.col_class ? a.col_class[c] : 0;
+                    int mi = qi < 0 ? -qi : qi;
+                    code = a.jtab[(int64_t)cls * 256 + mi];
+                    if (!asym && qi < 0) code |= 0x80;
+                }
+                a.code[r * a.code_ld + c] = code;
+            }
+            rsum += q;                            // exact: integers below 2^24
+        }
+        if (a.code)
+            for (int64_t c = a.cols + lane; c < a.code_ld; c += 64) a.code[r * a.code_ld + c] = 0;
+        if (a.rowsum) {
+            for (int o = 32; o > 0; o >>= 1) rsum += __shfl_xor(rsum, o, 64);
+            if (lane == 0) a.rowsum[r] = rsum;
+        }
+        if (lane < nseg && (a.scale || a.inv)) {
+            for (int64_t sgi = lane; sgi < nseg; sgi += 64) {
+                const QParams p = prm[g * nseg + sgi];
+                if (a.scale) a.scale[sgi * a.rows + r] = p.s;
+                if (a.inv) a.inv[sgi * a.rows + r] = p.inv;
+            }
+        }
+        if (lane == 0 && a.zp) a.zp[r] = prm[g * nseg].zp;
+    }
+}
+
+__global__ void tensor_out_kernel(const QParams *prm, double *scale64, double *zp64) {
+    if (scale64) scale64[0] = prm[0].s64;
+    if (zp64) zp64[0] = prm[0].zp64;
+}
+
+static inline void unit_counts(int64_t rows, int64_t cols, int64_t group, int64_t seg,
+                               int64_t *g, int64_t *segw, int64_t *nseg) {
+    int64_t G = group <= 0 || group > rows ? rows : group;
+    *g = G;
+    *segw = seg > 0 && seg < cols ? seg : (cols > 0 ? cols : 1);
+    *nseg = cdiv(cols > 0 ? cols : 1, *segw);
+}
+
+}  // namespace scmp
+
+using namespace scmp;
+
+extern "C" {
+
+int64_t scmp_quant_workspace_bytes(int64_t rows, int64_t cols, int64_t group, int64_t seg) {
+    int64_t G, segw, nseg;
+    unit_counts(rows, cols, group, seg, &G, &segw, &nseg);
+    int64_t nunits = cdiv(rows, G) * nseg;
+    return nunits * (int64_t)(2 * sizeof(uint32_t) + sizeof(QParams)) + 256;
+}
+
+int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
+    SCMP_REQUIRE(args != nullptr, "scmp_quantize: null args");
+    scmp_quant_args a = *args;
+    SCMP_REQUIRE(a.x && a.rows > 0 && a.cols > 0 && a.ld >= a.cols,
+                 "scmp_quantize: bad input shape rows=%lld cols=%lld ld=%lld",
+                 (long long)a.rows, (long long)a.cols, (long long)a.ld);
+    SCMP_REQUIRE(a.variant >= SCMP_Q_GROUP_SYM && a.variant <= SCMP_Q_TENSOR_ASYM,
+                 "scmp_quantize: unknown variant %d", a.variant);
+    SCMP_REQUIRE(a.q_max >= 1 && a.q_max <= 255, "scmp_quantize: q_max=%d outside [1, 255]",
+                 a.q_max);
+    SCMP_REQUIRE(a.workspace != nullptr, "scmp_quantize: workspace required");
+    SCMP_REQUIRE(a.smooth_mode == SCMP_SMOOTH_NONE || a.smooth != nullptr,
+                 "scmp_quantize: smooth_mode set without smooth vector");
+    if (a.code) {
+        SCMP_REQUIRE(a.code_ld >= a.cols && a.code_rows >= a.rows,
+                     "scmp_quantize: code buffer %lldx%lld smaller than input",
+                     (long long)a.code_rows, (long long)a.code_ld);
+        SCMP_REQUIRE(a.code_kind == SCMP_CODE_Q || (a.code_kind == SCMP_CODE_THERMO && a.jtab),
+                     "scmp_quantize: THERMO codes need jtab");
+    }
+    if (a.beta16 || a.beta32 || a.sign || a.xint)
+        SCMP_REQUIRE(a.out_ld >= a.cols, "scmp_quantize: out_ld < cols");
+    int64_t G, segw, nseg;
+    unit_counts(a.rows, a.cols, a.group, a.seg, &G, &segw, &nseg);
+    if (a.variant == SCMP_Q_TENSOR_SYM || a.variant == SCMP_Q_TENSOR_ASYM) {
+        G = a.rows;
+        segw = a.cols;
+        nseg = 1;
+    }
+    int64_t nunits = cdiv(a.rows, G) * nseg;
+    uint32_t *stats = (uint32_t *)a.workspace;
+    uintptr_t pa = ((uintptr_t)(stats + 2 * nunits) + 63) & ~(uintptr_t)63;
+    QParams *prm = (QParams *)pa;
+
+    stats_init_kernel<<<cdiv(2 * nunits, 256), 256, 0, stream>>>(stats, 2 * nunits);
+    SCMP_LAUNCH_CHECK("scmp_quantize/init");
+    int64_t ntask = a.rows * nseg;
+    int64_t blocks = cdiv(ntask, 4);
+    if (blocks > 8192) blocks = 8192;
+    reduce_kernel<<<blocks, 256, 0, stream>>>(a, G, segw, nseg, stats);
+    SCMP_LAUNCH_CHECK("scmp_quantize/reduce");
+    finalize_kernel<<<cdiv(nunits, 256), 256, 0, stream>>>(a, nunits, stats, prm);
+    SCMP_LAUNCH_CHECK("scmp_quantize/finalize");
+    int64_t nr = a.code && a.code_rows > a.rows ? a.code_rows : a.rows;
+    int64_t qblocks = cdiv(nr, 4);
+    if (qblocks > 16384) qblocks = 16384;
+    quantize_kernel<<<qblocks, 256, 0, stream>>>(a, G, segw, nseg, prm);
+    SCMP_LAUNCH_CHECK("scmp_quantize/quantize");
+    if (a.scale64 || a.zp64) {
+        tensor_out_kernel<<<1, 1, 0, stream>>>(prm, a.scale64, a.zp64);
+        SCMP_LAUNCH_CHECK("scmp_quantize/tensor_out");
+    }
+    return SCMP_OK;
+}
+
+}  // extern "C"
