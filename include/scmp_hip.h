@@ -98,6 +98,8 @@ int scmp_build_stream_tables(const int32_t *ra, const int32_t *rb, const int32_t
 #define SCMP_Q_HEAD_SYM 3     /* fused batched per-head: clamp [-(Q+1), Q], zero sign 0 */
 #define SCMP_Q_GROUP_ASYM 4   /* _grouped_asymmetric_quant: q = rne(fl(x / s) + zp) */
 #define SCMP_Q_TENSOR_ASYM 5  /* fused per-tensor unipolar (float64 scale/zp) */
+#define SCMP_Q_HOST_SYM 6     /* fused flat bipolar with the caller's fp32 reciprocal */
+#define SCMP_Q_HOST_ASYM 7    /* fused unipolar with the caller's fp32 reciprocal and zp */
 
 /* SmoothQuant fused into the load (apply_smoothing, scmp_kernels/quant/smoothquant.py:
  * 124-126): x' = fl(x / s[col]) (DIV) or fl(x * s[col]) (MUL). */
@@ -119,13 +121,15 @@ typedef struct scmp_quant_args {
     int variant;              /* SCMP_Q_* */
     int64_t group;            /* rows per group (>= rows: one group) */
     int64_t seg;              /* columns per segment (chunk_d); 0 = whole row */
-    int q_max;                /* Q */
+    int q_max;                /* Q (<= 255 when codes are written) */
     int rng_levels;           /* R, for the boundary outputs */
-    /* GEMM codes: code[row * code_ld + col], rows padded to code_rows and columns to
-     * code_ld with zero codes */
+    float host_inv, host_zp;  /* HOST_* variants: reciprocal scale and zero-point */
+    /* GEMM codes: the input rows form batches of code_batch_rows rows (0: one batch);
+     * batch b, row i goes to code[(b * code_rows + i) * code_ld + col]; rows
+     * code_batch_rows..code_rows-1 of every batch and columns cols..code_ld-1 are zero */
     int code_kind;
     uint8_t *code;
-    int64_t code_ld, code_rows;
+    int64_t code_ld, code_rows, code_batch_rows;
     const uint8_t *jtab;      /* THERMO: nclass x 256 */
     const int32_t *col_class; /* THERMO: class of each column, NULL = class 0 */
     /* reference API outputs (each optional) */

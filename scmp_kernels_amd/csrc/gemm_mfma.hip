@@ -239,7 +239,7 @@ sc_gemm_mfma_kernel(GemmP P) {
 __global__ void epilogue_kernel(const int32_t *iin, float *y, int N, int M, int64_t ldy,
                                 int64_t bsy, scmp_epilogue E) {
     const int batch = blockIdx.z;
-    const int n = blockIdx.y;
+    for (int n = blockIdx.y; n < N; n += gridDim.y)
     for (int m = blockIdx.x * blockDim.x + threadIdx.x; m < M; m += gridDim.x * blockDim.x) {
         const int64_t o = batch * bsy + (int64_t)n * ldy + m;
         const float I = (float)iin[o];
@@ -290,7 +290,7 @@ int run_epilogue(const int32_t *iin, float *y, int64_t N, int64_t M, int64_t bat
                  int64_t ldy, int64_t bsy, const scmp_epilogue &E, hipStream_t stream) {
     int64_t bx = cdiv(M, 256);
     if (bx > 64) bx = 64;
-    dim3 grid((unsigned)bx, (unsigned)N, (unsigned)batch);
+    dim3 grid((unsigned)bx, (unsigned)(N < 32768 ? N : 32768), (unsigned)batch);
     epilogue_kernel<<<grid, 256, 0, stream>>>(iin, y, (int)N, (int)M, ldy, bsy, E);
     SCMP_LAUNCH_CHECK("scmp_sc_gemm(epilogue)");
     return SCMP_OK;
@@ -344,7 +344,8 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     SCMP_REQUIRE(a.N > 0 && a.M > 0 && a.D > 0 && a.batch > 0,
                  "scmp_sc_gemm: empty problem N=%lld M=%lld D=%lld batch=%lld",
                  (long long)a.N, (long long)a.M, (long long)a.D, (long long)a.batch);
-    SCMP_REQUIRE(a.N < (1LL << 30) && a.M < (1LL << 30) && a.D < (1LL << 24),
+    SCMP_REQUIRE(a.N < (1LL << 30) && a.M < (1LL << 30) && a.D < (1LL << 24) &&
+                     a.batch < 65536,
                  "scmp_sc_gemm: dimensions too large");
     SCMP_REQUIRE(a.JP == 16 || a.JP == 32 || a.JP == 64 || a.JP == 128 || a.JP == 256,
                  "scmp_sc_gemm: JP=%d must be 16, 32, 64, 128 or 256", a.JP);

@@ -36,8 +36,9 @@ __device__ __forceinline__ float load_x(const scmp_quant_args &a, int64_t r, int
     return v;
 }
 
-__device__ __forceinline__ bool is_asym(int variant) {
-    return variant == SCMP_Q_GROUP_ASYM || variant == SCMP_Q_TENSOR_ASYM;
+__device__ __host__ __forceinline__ bool is_asym(int variant) {
+    return variant == SCMP_Q_GROUP_ASYM || variant == SCMP_Q_TENSOR_ASYM ||
+           variant == SCMP_Q_HOST_ASYM;
 }
 
 __global__ void stats_init_kernel(uint32_t *stats, int64_t n) {
@@ -133,6 +134,13 @@ __global__ void finalize_kernel(scmp_quant_args a, int64_t nunits, const uint32_
         p.zp64 = (double)p.zp;
         break;
     }
+    case SCMP_Q_HOST_SYM:
+    case SCMP_Q_HOST_ASYM:
+        // the caller computed scale / reciprocal / zero-point in Python floats
+        // (quant/fused.py:172-174, 204-209) and passes them rounded to fp32
+        p.inv = a.host_inv;
+        p.zp = a.host_zp;
+        break;
     case SCMP_Q_TENSOR_ASYM: {
         // quant/fused.py:204-209 in Python floats
         double mx = (double)float_of_key(stats[u * 2]);
@@ -157,16 +165,25 @@ __global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, 
     const int lane = threadIdx.x & 63;
     const int64_t wave = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) >> 6;
     const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
-    const int64_t nrows_total = a.code && a.code_rows > a.rows ? a.code_rows : a.rows;
+    // rows visited: every code row when codes are written (padding rows get zeros),
+    // otherwise every input row
+    const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+    const int64_t nbatch = a.code ? a.rows / cbr : 1;
+    const int64_t nrows_total = a.code ? nbatch * a.code_rows : a.rows;
     const float qf = (float)a.q_max;
     const bool asym = is_asym(a.variant);
     const float qlo = asym ? 0.0f : (a.variant == SCMP_Q_HEAD_SYM ? -(qf + 1.0f) : -qf);
     const float rq = __fdiv_rn((float)a.rng_levels, qf);
     const float rf = (float)a.rng_levels;
-    for (int64_t r = wave; r < nrows_total; r += nwaves) {
-        if (r >= a.rows) {                       // zero code rows of the GEMM padding
-            for (int64_t c = lane; c < a.code_ld; c += 64) a.code[r * a.code_ld + c] = 0;
-            continue;
+    for (int64_t vr = wave; vr < nrows_total; vr += nwaves) {
+        int64_t r = vr, crow = vr;
+        if (a.code) {
+            const int64_t b = vr / a.code_rows, i = vr - b * a.code_rows;
+            if (i >= cbr) {                      // zero code rows of the GEMM padding
+                for (int64_t c = lane; c < a.code_ld; c += 64) a.code[vr * a.code_ld + c] = 0;
+                continue;
+            }
+            r = b * cbr + i;
         }
         const int64_t g = r / group;
         float rsum = 0.0f;
@@ -178,7 +195,8 @@ __global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, 
             switch (a.variant) {
             case SCMP_Q_GROUP_SYM: t = __fdiv_rn(v, p.s); break;
             case SCMP_Q_GROUP_ASYM: t = __fadd_rn(__fdiv_rn(v, p.s), p.zp); break;
-            case SCMP_Q_TENSOR_ASYM: t = __fadd_rn(__fmul_rn(v, p.inv), p.zp); break;
+            case SCMP_Q_TENSOR_ASYM:
+            case SCMP_Q_HOST_ASYM: t = __fadd_rn(__fmul_rn(v, p.inv), p.zp); break;
             default: t = __fmul_rn(v, p.inv); break;
             }
             float q = fmin_first(fmax_first(rne(t), qlo), qf);
@@ -209,12 +227,12 @@ __global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, 
                     code = a.jtab[(int64_t)cls * 256 + mi];
                     if (!asym && qi < 0) code |= 0x80;
                 }
-                a.code[r * a.code_ld + c] = code;
+                a.code[crow * a.code_ld + c] = code;
             }
             rsum += q;                            // exact: integers below 2^24
         }
         if (a.code)
-            for (int64_t c = a.cols + lane; c < a.code_ld; c += 64) a.code[r * a.code_ld + c] = 0;
+            for (int64_t c = a.cols + lane; c < a.code_ld; c += 64) a.code[crow * a.code_ld + c] = 0;
         if (a.rowsum) {
             for (int o = 32; o > 0; o >>= 1) rsum += __shfl_xor(rsum, o, 64);
             if (lane == 0) a.rowsum[r] = rsum;
@@ -262,16 +280,21 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
     SCMP_REQUIRE(a.x && a.rows > 0 && a.cols > 0 && a.ld >= a.cols,
                  "scmp_quantize: bad input shape rows=%lld cols=%lld ld=%lld",
                  (long long)a.rows, (long long)a.cols, (long long)a.ld);
-    SCMP_REQUIRE(a.variant >= SCMP_Q_GROUP_SYM && a.variant <= SCMP_Q_TENSOR_ASYM,
+    SCMP_REQUIRE(a.variant >= SCMP_Q_GROUP_SYM && a.variant <= SCMP_Q_HOST_ASYM,
                  "scmp_quantize: unknown variant %d", a.variant);
-    SCMP_REQUIRE(a.q_max >= 1 && a.q_max <= 255, "scmp_quantize: q_max=%d outside [1, 255]",
+    SCMP_REQUIRE(a.q_max >= 1 && a.q_max < (1 << 24), "scmp_quantize: q_max=%d out of range",
                  a.q_max);
+    SCMP_REQUIRE(!a.code || a.q_max <= 255,
+                 "scmp_quantize: GEMM codes need q_max <= 255 (got %d)", a.q_max);
     SCMP_REQUIRE(a.workspace != nullptr, "scmp_quantize: workspace required");
     SCMP_REQUIRE(a.smooth_mode == SCMP_SMOOTH_NONE || a.smooth != nullptr,
                  "scmp_quantize: smooth_mode set without smooth vector");
     if (a.code) {
-        SCMP_REQUIRE(a.code_ld >= a.cols && a.code_rows >= a.rows,
-                     "scmp_quantize: code buffer %lldx%lld smaller than input",
+        const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+        SCMP_REQUIRE(a.rows % cbr == 0, "scmp_quantize: rows %lld not a multiple of the "
+                     "batch rows %lld", (long long)a.rows, (long long)cbr);
+        SCMP_REQUIRE(a.code_ld >= a.cols && a.code_rows >= cbr,
+                     "scmp_quantize: code buffer rows/ld (%lld, %lld) smaller than the input",
                      (long long)a.code_rows, (long long)a.code_ld);
         SCMP_REQUIRE(a.code_kind == SCMP_CODE_Q || (a.code_kind == SCMP_CODE_THERMO && a.jtab),
                      "scmp_quantize: THERMO codes need jtab");
@@ -280,7 +303,8 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
         SCMP_REQUIRE(a.out_ld >= a.cols, "scmp_quantize: out_ld < cols");
     int64_t G, segw, nseg;
     unit_counts(a.rows, a.cols, a.group, a.seg, &G, &segw, &nseg);
-    if (a.variant == SCMP_Q_TENSOR_SYM || a.variant == SCMP_Q_TENSOR_ASYM) {
+    if (a.variant == SCMP_Q_TENSOR_SYM || a.variant == SCMP_Q_TENSOR_ASYM ||
+        a.variant == SCMP_Q_HOST_SYM || a.variant == SCMP_Q_HOST_ASYM) {
         G = a.rows;
         segw = a.cols;
         nseg = 1;
@@ -290,16 +314,20 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
     uintptr_t pa = ((uintptr_t)(stats + 2 * nunits) + 63) & ~(uintptr_t)63;
     QParams *prm = (QParams *)pa;
 
-    stats_init_kernel<<<cdiv(2 * nunits, 256), 256, 0, stream>>>(stats, 2 * nunits);
-    SCMP_LAUNCH_CHECK("scmp_quantize/init");
-    int64_t ntask = a.rows * nseg;
-    int64_t blocks = cdiv(ntask, 4);
-    if (blocks > 8192) blocks = 8192;
-    reduce_kernel<<<blocks, 256, 0, stream>>>(a, G, segw, nseg, stats);
-    SCMP_LAUNCH_CHECK("scmp_quantize/reduce");
+    const bool host = a.variant == SCMP_Q_HOST_SYM || a.variant == SCMP_Q_HOST_ASYM;
+    if (!host) {
+        stats_init_kernel<<<cdiv(2 * nunits, 256), 256, 0, stream>>>(stats, 2 * nunits);
+        SCMP_LAUNCH_CHECK("scmp_quantize/init");
+        int64_t ntask = a.rows * nseg;
+        int64_t blocks = cdiv(ntask, 4);
+        if (blocks > 8192) blocks = 8192;
+        reduce_kernel<<<blocks, 256, 0, stream>>>(a, G, segw, nseg, stats);
+        SCMP_LAUNCH_CHECK("scmp_quantize/reduce");
+    }
     finalize_kernel<<<cdiv(nunits, 256), 256, 0, stream>>>(a, nunits, stats, prm);
     SCMP_LAUNCH_CHECK("scmp_quantize/finalize");
-    int64_t nr = a.code && a.code_rows > a.rows ? a.code_rows : a.rows;
+    const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+    int64_t nr = a.code ? (a.rows / cbr) * a.code_rows : a.rows;
     int64_t qblocks = cdiv(nr, 4);
     if (qblocks > 16384) qblocks = 16384;
     quantize_kernel<<<qblocks, 256, 0, stream>>>(a, G, segw, nseg, prm);

@@ -1,0 +1,11 @@
+"""Stochastic-computing matmul on MI355X (the reference's scmp_kernels.sc surface,
+scmp_kernels/sc/__init__.py:20-27).
+
+* ``sc_matmul`` — unified granularity dispatcher.
+* ``clear_rng_cache`` — drop cached RNG sequences and stream tables.
+* ``det_kernel_tuning`` — re-entrant context manager (API compatibility).
+"""
+from .matmul import sc_matmul
+from .kernels import clear_rng_cache, det_kernel_tuning
+
+__all__ = ["sc_matmul", "clear_rng_cache", "det_kernel_tuning"]

@@ -1,0 +1,494 @@
+"""Host orchestration of the SC matmul on gfx950 (PyTorch tensors for memory and streams,
+libscmp_hip.so for every kernel).
+
+Each path mirrors one host function of the reference (scmp_kernels/sc/kernels.py) and
+keeps its numerics: the same quantizer variant, boundary grid, stream tables and fp32
+epilogue order. The pipeline per call is
+
+    quantize(a) -> A codes (thermometer lengths), quantize(b) -> B codes (q bytes)
+    SC GEMM (int8 MFMA, exact int32 accumulator) -> fp32 epilogue
+
+with SmoothQuant's a/s, b*s folded into the quantizer loads. Per-tensor ranges are
+reduced on the device (no host synchronization); the scale products that the reference
+forms in Python floats are formed in float64 on the device.
+
+The FP->int quantizer API of the reference is re-exported here under its original names
+(scmp_kernels/sc/kernels.py:42-52).
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import numpy as np
+import torch
+
+from .. import _lib
+from ..quant import (  # noqa: F401  (re-exports, scmp_kernels/sc/kernels.py:42-52)
+    fused_quant_kernel,
+    fused_quant_bipolar_batched_kernel,
+    fused_quantize_bipolar,
+    fused_quantize_bipolar_perrow,
+    fused_quantize_unipolar,
+    _quant_dummy,
+    _grouped_symmetric_quant,
+    _grouped_asymmetric_quant,
+    _grouped_symmetric_quant_batched,
+)
+from . import tables as _tables
+from .config_helpers import make_sobol_simple_config
+
+ROW_PAD = 256      # GEMM workgroup tile rows: code buffers are padded to this
+
+
+def clear_rng_cache():
+    """Clear the cached RNG sequences and stream tables (kernels.py:90-94)."""
+    _tables.clear()
+
+
+def _resolve_rng_levels(sc_prec: int, rng_levels: Optional[int]) -> int:
+    """scmp_kernels/sc/kernels.py:596-606."""
+    if rng_levels is None:
+        return 2 ** sc_prec
+    return int(rng_levels)
+
+
+# -------------------------------------------------------------------------------------
+# det kernel tuning (scmp_kernels/sc/kernels.py:1728-1745): a re-entrant context manager
+# that the reference never consults when choosing tiles; kept for API compatibility.
+# -------------------------------------------------------------------------------------
+
+_DET_KERNEL_TUNING_DEPTH = 0
+
+
+class det_kernel_tuning:
+    """Re-entrant context manager opting in to det-tuned tile selection (no effect on the
+    results; tiles here are chosen by problem shape)."""
+
+    def __enter__(self):
+        global _DET_KERNEL_TUNING_DEPTH
+        _DET_KERNEL_TUNING_DEPTH += 1
+        return self
+
+    def __exit__(self, *_):
+        global _DET_KERNEL_TUNING_DEPTH
+        _DET_KERNEL_TUNING_DEPTH -= 1
+
+
+def _det_kernel_tuning_active() -> bool:
+    return _DET_KERNEL_TUNING_DEPTH > 0
+
+
+# -------------------------------------------------------------------------------------
+# low-level launch helpers
+# -------------------------------------------------------------------------------------
+
+def _round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+def _rows2d(x: torch.Tensor) -> torch.Tensor:
+    """fp32 2-D view with unit column stride (copies only when needed)."""
+    if x.dtype != torch.float32:
+        x = x.float()
+    if x.dim() != 2:
+        x = x.reshape(-1, x.shape[-1])
+    if x.stride(-1) != 1 or x.stride(0) < x.shape[1]:
+        x = x.contiguous()
+    return x
+
+
+def _workspace(rows, cols, group, seg, device):
+    nbytes = int(_lib.load().scmp_quant_workspace_bytes(rows, cols, group, seg))
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def quantize(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, *, group: int = 1,
+             seg: int = 0, smooth: Optional[torch.Tensor] = None, smooth_mode: int = 0,
+             code: Optional[torch.Tensor] = None, code_kind: int = 0,
+             code_batch_rows: int = 0, jtab=None, col_class=None, beta16=None, beta32=None,
+             beta_formula: int = 0, sign=None, xint=None, scale=None, scale64=None, inv=None,
+             zp=None, zp64=None, rowsum=None, host_inv: float = 0.0, host_zp: float = 0.0):
+    """One scmp_quantize call on the current stream; outputs are written in place."""
+    x = _rows2d(x)
+    rows, cols = x.shape
+    G = rows if group <= 0 or group > rows else group
+    a = _lib.QuantArgs()
+    a.x, a.rows, a.cols, a.ld = x.data_ptr(), rows, cols, x.stride(0)
+    a.smooth, a.smooth_mode = _lib.ptr(smooth), smooth_mode
+    a.variant, a.group, a.seg = variant, G, seg
+    a.q_max, a.rng_levels = q_max, rng_levels
+    a.host_inv, a.host_zp = host_inv, host_zp
+    a.code_kind, a.code = code_kind, _lib.ptr(code)
+    if code is not None:
+        a.code_ld, a.code_rows = code.shape[-1], code.shape[-2]
+    a.code_batch_rows = code_batch_rows
+    a.jtab, a.col_class = _lib.ptr(jtab), _lib.ptr(col_class)
+    a.beta16, a.beta32, a.beta_formula = _lib.ptr(beta16), _lib.ptr(beta32), beta_formula
+    a.sign, a.xint, a.out_ld = _lib.ptr(sign), _lib.ptr(xint), cols
+    a.scale, a.scale64, a.inv = _lib.ptr(scale), _lib.ptr(scale64), _lib.ptr(inv)
+    a.zp, a.zp64, a.rowsum = _lib.ptr(zp), _lib.ptr(zp64), _lib.ptr(rowsum)
+    ws = _workspace(rows, cols, G, seg, x.device)
+    a.workspace = ws.data_ptr()
+    _lib.check(_lib.load().scmp_quantize(a, _lib.stream_of(x.device)), "scmp_quantize")
+    return ws  # keep the workspace alive until the stream has consumed it
+
+
+def _gemm_impl() -> int:
+    return _lib.GEMM_VALU if os.environ.get("SCMP_GEMM_IMPL", "mfma").lower() == "valu" \
+        else _lib.GEMM_MFMA
+
+
+def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.Epilogue",
+            y=None, iout=None, ldy=None, bsy=0, chunk=0, d_class=None, impl=None, tile=None):
+    """scmp_sc_gemm on the current stream. ca / cb are code buffers (batch, rows_pad, ld)
+    or (rows_pad, ld)."""
+    g = _lib.GemmArgs()
+    g.ca, g.lda = ca.data_ptr(), ca.shape[-1]
+    g.bsa = ca.shape[-2] * ca.shape[-1] if ca.dim() == 3 else 0
+    g.cb, g.ldb = cb.data_ptr(), cb.shape[-1]
+    g.bsb = cb.shape[-2] * cb.shape[-1] if cb.dim() == 3 else 0
+    g.N, g.M, g.D, g.batch = N, M, D, batch
+    g.bipolar, g.JP = 1 if tabs.bipolar else 0, tabs.JP
+    g.lut = tabs.lut.data_ptr()
+    dc = d_class if d_class is not None else tabs.d_class
+    g.d_class = _lib.ptr(dc)
+    g.chunk = chunk
+    g.epi = epi
+    g.y, g.iout = _lib.ptr(y), _lib.ptr(iout)
+    g.ldy = ldy if ldy is not None else M
+    g.bsy = bsy
+    g.impl = _gemm_impl() if impl is None else impl
+    g.tile = int(os.environ.get("SCMP_GEMM_TILE", "0")) if tile is None else tile
+    dev = ca.device
+    if g.impl == _lib.GEMM_VALU:
+        g.bitlut = tabs.bitlut(_lib.stream_of(dev)).data_ptr()
+    _lib.check(_lib.load().scmp_sc_gemm(g, _lib.stream_of(dev)), "scmp_sc_gemm")
+
+
+def _codes(rows: int, D: int, device, batch: int = 0) -> torch.Tensor:
+    """Uninitialized code buffer; the quantizer fills it including the zero padding."""
+    shape = (_round_up(rows, ROW_PAD), _round_up(D, 16))
+    if batch:
+        shape = (batch,) + shape
+    return torch.empty(shape, dtype=torch.uint8, device=device)
+
+
+def _inner_scale(Q: int, L: int) -> float:
+    """q_max_sq / stoc_len evaluated in fp32 (kernels.py:212)."""
+    return float(np.float32(np.float32(Q * Q) / np.float32(L)))
+
+
+def _get_tables(config, sc_prec, L, R, bipolar, D, device):
+    return _tables.get_tables(config, ("sobol_simple", D, D, sc_prec),
+                              lambda: make_sobol_simple_config(D, D, sc_prec),
+                              sc_prec, L, R, bipolar, D, device)
+
+
+def _smooth_args(smooth: Optional[torch.Tensor], side: str):
+    if smooth is None:
+        return None, _lib.SMOOTH_NONE
+    return smooth, (_lib.SMOOTH_DIV if side == "a" else _lib.SMOOTH_MUL)
+
+
+def _check_gpu(a: torch.Tensor):
+    if not a.is_cuda:
+        raise RuntimeError("scmp_kernels_amd: the SC kernels run on the GPU; got CPU tensors "
+                           "and no GPU is available")
+
+
+def _to_gpu(a: torch.Tensor, b: torch.Tensor):
+    """CPU inputs are moved to the GPU and results back (kernels.py:1115-1117,
+    1150-1151)."""
+    if a.is_cuda:
+        return a, b, None
+    if not torch.cuda.is_available():
+        raise RuntimeError("scmp_kernels_amd: the SC kernels run on the GPU; got CPU tensors "
+                           "and no GPU is available")
+    return a.cuda(), b.cuda(), a.device
+
+
+# -------------------------------------------------------------------------------------
+# per_row, 2-D  (scmp_kernels/sc/kernels.py:1574-1707)
+# -------------------------------------------------------------------------------------
+
+@torch.no_grad()
+def _sc_matmul_per_row(a, b, group_a=1, group_b=1, mode="unipolar", sc_prec=8, config=None,
+                       stoc_len=None, rng_levels=None, smooth_scales=None):
+    if stoc_len is None:
+        stoc_len = 2 ** sc_prec
+    assert a.dim() == 2 and b.dim() == 2, f"Expected 2D, got a:{a.dim()}D b:{b.dim()}D"
+    assert a.shape[1] == b.shape[1], f"Inner dim mismatch: {a.shape[1]} vs {b.shape[1]}"
+    if mode not in ("bipolar", "unipolar"):
+        raise ValueError(f"Unknown mode: {mode}")
+    a, b, home = _to_gpu(a, b)
+    N, D = a.shape
+    M = b.shape[0]
+    R = _resolve_rng_levels(sc_prec, rng_levels)
+    dev = a.device
+    bip = mode == "bipolar"
+    tabs = _get_tables(config, sc_prec, stoc_len, R, bip, D, dev)
+    ca, cb = _codes(N, D, dev), _codes(M, D, dev)
+    sa = torch.empty(N, dtype=torch.float32, device=dev)
+    sb = torch.empty(M, dtype=torch.float32, device=dev)
+    y = torch.empty((N, M), dtype=torch.float32, device=dev)
+    s_a, m_a = _smooth_args(smooth_scales, "a")
+    s_b, m_b = _smooth_args(smooth_scales, "b")
+    epi = _lib.Epilogue()
+    if bip:
+        Q = 2 ** (sc_prec - 1) - 1
+        w1 = quantize(a, _lib.Q_GROUP_SYM, Q, R, group=group_a, smooth=s_a, smooth_mode=m_a,
+                      code=ca, code_kind=_lib.CODE_THERMO, jtab=tabs.jtab,
+                      col_class=tabs.d_class, scale=sa)
+        w2 = quantize(b, _lib.Q_GROUP_SYM, Q, R, group=group_b, smooth=s_b, smooth_mode=m_b,
+                      code=cb, code_kind=_lib.CODE_Q, scale=sb)
+        epi.kind, epi.c = _lib.EPI_ROWCOL, _inner_scale(Q, stoc_len)
+        epi.sa, epi.sb = sa.data_ptr(), sb.data_ptr()
+        sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, y=y)
+    else:
+        Q = 2 ** sc_prec - 1
+        za = torch.empty(N, dtype=torch.float32, device=dev)
+        zb = torch.empty(M, dtype=torch.float32, device=dev)
+        ra = torch.empty(N, dtype=torch.float32, device=dev)
+        rb = torch.empty(M, dtype=torch.float32, device=dev)
+        w1 = quantize(a, _lib.Q_GROUP_ASYM, Q, R, group=group_a, smooth=s_a, smooth_mode=m_a,
+                      code=ca, code_kind=_lib.CODE_THERMO, jtab=tabs.jtab,
+                      col_class=tabs.d_class, scale=sa, zp=za, rowsum=ra)
+        w2 = quantize(b, _lib.Q_GROUP_ASYM, Q, R, group=group_b, smooth=s_b, smooth_mode=m_b,
+                      code=cb, code_kind=_lib.CODE_Q, scale=sb, zp=zb, rowsum=rb)
+        epi.kind, epi.c = _lib.EPI_ZP_ROWCOL, _inner_scale(Q, stoc_len)
+        epi.sa, epi.sb, epi.za, epi.zb = sa.data_ptr(), sb.data_ptr(), za.data_ptr(), zb.data_ptr()
+        epi.suma, epi.sumb, epi.dfloat = ra.data_ptr(), rb.data_ptr(), float(np.float32(D))
+        sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, y=y)
+    del w1, w2
+    return y.to(home) if home is not None else y
+
+
+# -------------------------------------------------------------------------------------
+# per_row + chunk_d (scmp_kernels/sc/kernels.py:1444-1566, 1274-1383)
+# -------------------------------------------------------------------------------------
+
+@torch.no_grad()
+def _sc_matmul_per_row_mlp(a, b, mode="bipolar", sc_prec=8, config=None, group_a=1,
+                           group_b=1, chunk_d=0, stoc_len=None, rng_levels=None,
+                           smooth_scales=None):
+    if stoc_len is None:
+        stoc_len = 2 ** sc_prec
+    assert a.dim() == 2 and b.dim() == 2, f"Expected 2D, got a:{a.dim()}D b:{b.dim()}D"
+    assert a.shape[1] == b.shape[1], f"Dim mismatch: a={a.shape[1]}, b={b.shape[1]}"
+    N, D = a.shape
+    if not (mode == "bipolar" and chunk_d > 0 and D > chunk_d):
+        # standard path: the grouped quantizer arithmetic of _sc_matmul_per_row
+        return _sc_matmul_per_row(a, b, group_a=group_a, group_b=group_b, mode=mode,
+                                  sc_prec=sc_prec, config=config, stoc_len=stoc_len,
+                                  rng_levels=rng_levels, smooth_scales=smooth_scales)
+    a, b, home = _to_gpu(a, b)
+    M = b.shape[0]
+    dev = a.device
+    R = _resolve_rng_levels(sc_prec, rng_levels)
+    Q = 2 ** (sc_prec - 1) - 1
+    tabs = _tables.get_tables(config, ("sobol_simple", chunk_d, chunk_d, sc_prec),
+                              lambda: make_sobol_simple_config(chunk_d, chunk_d, sc_prec),
+                              sc_prec, stoc_len, R, True, chunk_d, dev)
+    if tabs.JP == 16 and chunk_d % 2:
+        raise NotImplementedError("sc_matmul: chunk_d must be even for stoc_len <= 16")
+    # dimension d of every chunk uses the tables of local index d mod chunk_d
+    d_class = None
+    if tabs.nclass > 1:
+        d_class = torch.from_numpy(tabs.class_of[np.arange(D) % chunk_d]).to(dev)
+    nseg = (D + chunk_d - 1) // chunk_d
+    ca, cb = _codes(N, D, dev), _codes(M, D, dev)
+    sa = torch.empty((nseg, N), dtype=torch.float32, device=dev)
+    sb = torch.empty((nseg, M), dtype=torch.float32, device=dev)
+    s_a, m_a = _smooth_args(smooth_scales, "a")
+    s_b, m_b = _smooth_args(smooth_scales, "b")
+    w1 = quantize(a, _lib.Q_ROW_SYM, Q, R, group=1, seg=chunk_d, smooth=s_a, smooth_mode=m_a,
+                  code=ca, code_kind=_lib.CODE_THERMO, jtab=tabs.jtab, col_class=d_class,
+                  scale=sa)
+    w2 = quantize(b, _lib.Q_ROW_SYM, Q, R, group=1, seg=chunk_d, smooth=s_b, smooth_mode=m_b,
+                  code=cb, code_kind=_lib.CODE_Q, scale=sb)
+    y = torch.empty((N, M), dtype=torch.float32, device=dev)
+    epi = _lib.Epilogue()
+    epi.kind, epi.c = _lib.EPI_ROWCOL, _inner_scale(Q, stoc_len)
+    epi.sa, epi.sb = sa.data_ptr(), sb.data_ptr()
+    epi.sa_chunk_stride, epi.sb_chunk_stride = N, M
+    sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, y=y, chunk=chunk_d,
+            d_class=d_class, impl=_lib.GEMM_MFMA)
+    del w1, w2
+    return y.to(home) if home is not None else y
+
+
+# -------------------------------------------------------------------------------------
+# per_row, 3-D (scmp_kernels/sc/kernels.py:1779-1895)
+# -------------------------------------------------------------------------------------
+
+@torch.no_grad()
+def _sc_matmul_per_row_batched(a, b, group_a=1, group_b=1, mode="bipolar", sc_prec=8,
+                               config=None, stoc_len=None, rng_levels=None,
+                               smooth_scales=None):
+    assert a.dim() == 3 and b.dim() == 3, f"Expected 3D, got a:{a.dim()}D b:{b.dim()}D"
+    BH, Ma, D = a.shape
+    BH_b, Nb, D_b = b.shape
+    assert BH == BH_b, f"batch mismatch: a BH={BH} vs b BH={BH_b}"
+    assert D == D_b, f"inner-dim mismatch: a D={D} vs b D={D_b}"
+    if stoc_len is None:
+        stoc_len = 2 ** sc_prec
+    a, b, home = _to_gpu(a, b)
+    dev = a.device
+    if mode == "unipolar":
+        out = torch.empty((BH, Ma, Nb), dtype=torch.float32, device=dev)
+        for i in range(BH):
+            out[i] = _sc_matmul_per_row(a[i], b[i], group_a=group_a, group_b=group_b,
+                                        mode=mode, sc_prec=sc_prec, config=config,
+                                        stoc_len=stoc_len, rng_levels=rng_levels,
+                                        smooth_scales=smooth_scales)
+        return out.to(home) if home is not None else out
+    if mode != "bipolar":
+        raise ValueError(f"Unknown mode: {mode}")
+
+    def group_of(G, rows):
+        if G >= rows:
+            return rows
+        if G == 1:
+            return 1
+        raise NotImplementedError(
+            f"_grouped_symmetric_quant_batched: G={G} not supported (use G=1 or G>=rows)")
+
+    ga, gb = group_of(group_a, Ma), group_of(group_b, Nb)
+    R = _resolve_rng_levels(sc_prec, rng_levels)
+    Q = 2 ** (sc_prec - 1) - 1
+    tabs = _get_tables(config, sc_prec, stoc_len, R, True, D, dev)
+    ca, cb = _codes(Ma, D, dev, batch=BH), _codes(Nb, D, dev, batch=BH)
+    sa = torch.empty(BH * Ma, dtype=torch.float32, device=dev)
+    sb = torch.empty(BH * Nb, dtype=torch.float32, device=dev)
+    s_a, m_a = _smooth_args(smooth_scales, "a")
+    s_b, m_b = _smooth_args(smooth_scales, "b")
+    w1 = quantize(a.reshape(BH * Ma, D), _lib.Q_GROUP_SYM, Q, R, group=ga, smooth=s_a,
+                  smooth_mode=m_a, code=ca, code_kind=_lib.CODE_THERMO, code_batch_rows=Ma,
+                  jtab=tabs.jtab, col_class=tabs.d_class, scale=sa)
+    w2 = quantize(b.reshape(BH * Nb, D), _lib.Q_GROUP_SYM, Q, R, group=gb, smooth=s_b,
+                  smooth_mode=m_b, code=cb, code_kind=_lib.CODE_Q, code_batch_rows=Nb,
+                  scale=sb)
+    y = torch.empty((BH, Ma, Nb), dtype=torch.float32, device=dev)
+    epi = _lib.Epilogue()
+    # acc *= inner_scale * 1.0 (head scale of ones, kernels.py:1877-1892) == fl(I * c)
+    epi.kind, epi.c = _lib.EPI_ROWCOL, _inner_scale(Q, stoc_len)
+    epi.sa, epi.sb = sa.data_ptr(), sb.data_ptr()
+    epi.sa_batch_stride, epi.sb_batch_stride = Ma, Nb
+    sc_gemm(ca, cb, N=Ma, M=Nb, D=D, batch=BH, tabs=tabs, epi=epi, y=y, bsy=Ma * Nb)
+    del w1, w2
+    return y.to(home) if home is not None else y
+
+
+# -------------------------------------------------------------------------------------
+# per_head bipolar (scmp_kernels/sc/kernels.py:440-585)
+# -------------------------------------------------------------------------------------
+
+@torch.no_grad()
+def _sc_matmul_per_head_bipolar(q_flat, k_flat, sc_prec, config, stoc_len=None,
+                                rng_levels=None, smooth_scales=None):
+    if stoc_len is None:
+        stoc_len = 2 ** sc_prec
+    BH, N, D = q_flat.shape
+    BH_k, M, D_k = k_flat.shape
+    if BH_k != BH or D_k != D:
+        raise ValueError(
+            f"_sc_matmul_per_head_bipolar: shape mismatch — q is (BH={BH}, N={N}, D={D}), "
+            f"k is (BH={BH_k}, M={M}, D={D_k}); require equal BH and D.")
+    q_flat, k_flat, home = _to_gpu(q_flat, k_flat)
+    dev = q_flat.device
+    Q = 2 ** (sc_prec - 1) - 1
+    R = _resolve_rng_levels(sc_prec, rng_levels)
+    tabs = _tables.get_tables(config, ("sobol_simple", D, D, sc_prec),
+                              lambda: make_sobol_simple_config(D, D, sc_prec),
+                              sc_prec, stoc_len, R, True, D, dev)
+    ca, cb = _codes(N, D, dev, batch=BH), _codes(M, D, dev, batch=BH)
+    sq = torch.empty(BH * N, dtype=torch.float32, device=dev)
+    sk = torch.empty(BH * M, dtype=torch.float32, device=dev)
+    s_a, m_a = _smooth_args(smooth_scales, "a")
+    s_b, m_b = _smooth_args(smooth_scales, "b")
+    w1 = quantize(q_flat.reshape(BH * N, D), _lib.Q_HEAD_SYM, Q, R, group=N, smooth=s_a,
+                  smooth_mode=m_a, code=ca, code_kind=_lib.CODE_THERMO, code_batch_rows=N,
+                  jtab=tabs.jtab, col_class=tabs.d_class, scale=sq)
+    w2 = quantize(k_flat.reshape(BH * M, D), _lib.Q_HEAD_SYM, Q, R, group=M, smooth=s_b,
+                  smooth_mode=m_b, code=cb, code_kind=_lib.CODE_Q, code_batch_rows=M, scale=sk)
+    # out_scale = scale_q * scale_k (kernels.py:550), fp32
+    hs = (sq[::N] * sk[::M]).contiguous()
+    y = torch.empty((BH, N, M), dtype=torch.float32, device=dev)
+    epi = _lib.Epilogue()
+    epi.kind, epi.c = _lib.EPI_HEAD, _inner_scale(Q, stoc_len)
+    epi.s = hs.data_ptr()
+    sc_gemm(ca, cb, N=N, M=M, D=D, batch=BH, tabs=tabs, epi=epi, y=y, bsy=N * M)
+    del w1, w2
+    return y.to(home) if home is not None else y
+
+
+# -------------------------------------------------------------------------------------
+# per_tensor (scmp_kernels/sc/kernels.py:1054-1226), ranges reduced on the device
+# -------------------------------------------------------------------------------------
+
+@torch.no_grad()
+def _sc_matmul_per_tensor(a, b, mode="bipolar", sc_prec=8, config=None, stoc_len=None,
+                          rng_levels=None, smooth_scales=None):
+    if stoc_len is None:
+        stoc_len = 2 ** sc_prec
+    if a.dim() == 3:
+        BH, N, D = a.shape
+        M = b.shape[1]
+        batch = BH
+    else:
+        assert a.dim() == 2 and b.dim() == 2, f"Expected 2D, got a:{a.dim()}D b:{b.dim()}D"
+        assert a.shape[1] == b.shape[1], f"Dim mismatch: a={a.shape[1]}, b={b.shape[1]}"
+        N, D = a.shape
+        M = b.shape[0]
+        batch = 0
+    if mode not in ("bipolar", "unipolar"):
+        raise ValueError(f"Unknown mode: {mode}")
+    a, b, home = _to_gpu(a, b)
+    dev = a.device
+    R = _resolve_rng_levels(sc_prec, rng_levels)
+    bip = mode == "bipolar"
+    tabs = _get_tables(config, sc_prec, stoc_len, R, bip, D, dev)
+    nb = max(batch, 1)
+    ca, cb = _codes(N, D, dev, batch=batch), _codes(M, D, dev, batch=batch)
+    a2, b2 = a.reshape(nb * N, D), b.reshape(nb * M, D)
+    s_a, m_a = _smooth_args(smooth_scales, "a")
+    s_b, m_b = _smooth_args(smooth_scales, "b")
+    sa64 = torch.empty(1, dtype=torch.float64, device=dev)
+    sb64 = torch.empty(1, dtype=torch.float64, device=dev)
+    y = torch.empty((batch, N, M) if batch else (N, M), dtype=torch.float32, device=dev)
+    epi = _lib.Epilogue()
+    if bip:
+        Q = 2 ** (sc_prec - 1) - 1
+        w1 = quantize(a2, _lib.Q_TENSOR_SYM, Q, R, smooth=s_a, smooth_mode=m_a, code=ca,
+                      code_kind=_lib.CODE_THERMO, code_batch_rows=N if batch else 0,
+                      jtab=tabs.jtab, col_class=tabs.d_class, scale64=sa64)
+        w2 = quantize(b2, _lib.Q_TENSOR_SYM, Q, R, smooth=s_b, smooth_mode=m_b, code=cb,
+                      code_kind=_lib.CODE_Q, code_batch_rows=M if batch else 0, scale64=sb64)
+        s = (sa64 * sb64).float()          # Python-float product -> fp32 (kernels.py:1204)
+        epi.kind, epi.c, epi.s = _lib.EPI_SCALAR, _inner_scale(Q, stoc_len), s.data_ptr()
+        sc_gemm(ca, cb, N=N, M=M, D=D, batch=nb, tabs=tabs, epi=epi, y=y, bsy=N * M)
+    else:
+        Q = 2 ** sc_prec - 1
+        za = torch.empty(nb * N, dtype=torch.float32, device=dev)
+        zb = torch.empty(nb * M, dtype=torch.float32, device=dev)
+        za64 = torch.empty(1, dtype=torch.float64, device=dev)
+        zb64 = torch.empty(1, dtype=torch.float64, device=dev)
+        ra = torch.empty(nb * N, dtype=torch.float32, device=dev)
+        rb = torch.empty(nb * M, dtype=torch.float32, device=dev)
+        w1 = quantize(a2, _lib.Q_TENSOR_ASYM, Q, R, smooth=s_a, smooth_mode=m_a, code=ca,
+                      code_kind=_lib.CODE_THERMO, code_batch_rows=N if batch else 0,
+                      jtab=tabs.jtab, col_class=tabs.d_class, scale64=sa64, zp=za,
+                      zp64=za64, rowsum=ra)
+        w2 = quantize(b2, _lib.Q_TENSOR_ASYM, Q, R, smooth=s_b, smooth_mode=m_b, code=cb,
+                      code_kind=_lib.CODE_Q, code_batch_rows=M if batch else 0, scale64=sb64,
+                      zp=zb, zp64=zb64, rowsum=rb)
+        s = (sa64 * sb64).float()
+        t3 = ((D * za64) * zb64).float()   # Python float D * zp_a * zp_b (kernels.py:1202)
+        epi.kind, epi.c = _lib.EPI_ZP_SCALAR, _inner_scale(Q, stoc_len)
+        epi.s, epi.za, epi.zb, epi.t3 = s.data_ptr(), za.data_ptr(), zb.data_ptr(), t3.data_ptr()
+        epi.suma, epi.sumb = ra.data_ptr(), rb.data_ptr()
+        epi.sa_batch_stride, epi.sb_batch_stride = N, M
+        sc_gemm(ca, cb, N=N, M=M, D=D, batch=nb, tabs=tabs, epi=epi, y=y, bsy=N * M)
+    del w1, w2
+    return y.to(home) if home is not None else y

@@ -1,0 +1,350 @@
+"""GPU parity: every HIP kernel (through the C ABI) against the CPU oracle on the same
+seeded inputs, and sc_matmul against the reference's golden vectors. Bit-exact: integer
+sequences, tables, quantized codes and accumulators; fp32 outputs compared bitwise."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sc_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _dev():
+    return torch.device("cuda", 0)
+
+
+def T(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(_dev())
+
+
+def bits_equal(got: torch.Tensor, ref: np.ndarray):
+    g = got.detach().cpu().numpy()
+    assert g.shape == ref.shape, (g.shape, ref.shape)
+    if g.dtype.kind == "f":
+        g = g.astype(ref.dtype)
+        bad = g.view(np.uint8 if g.itemsize == 1 else np.uint32 if g.itemsize == 4 else np.uint64) \
+            != ref.view(np.uint8 if ref.itemsize == 1 else np.uint32 if ref.itemsize == 4 else np.uint64)
+    else:
+        bad = g != ref
+    n = int(np.count_nonzero(bad))
+    assert n == 0, f"{n} of {bad.size} elements differ; first at {np.argwhere(bad)[0].tolist()}"
+
+
+# -------------------------------------------------------------------------------------
+# RNG sequences, prefix/Owen/rescale, stream tables
+# -------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("p", [4, 6, 8])
+@pytest.mark.parametrize("seed_type", ["q", "k"])
+def test_sobol_sequence(p, seed_type):
+    from scmp_kernels_amd.sc.rng import Sobol
+    got = Sobol(p, seed_type=seed_type).simulate()
+    ref = O.sobol_sequence(p, O.sobol_default_seed(p, seed_type), 2 ** p)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_sobol_custom_seed_and_lfsr():
+    from scmp_kernels_amd.sc.rng import Sobol, LFSR
+    seed = [1, 3, 7, 15, 31, 63, 127, 255]
+    np.testing.assert_array_equal(Sobol(8, seed=seed).simulate(),
+                                  O.sobol_sequence(8, seed, 256))
+    for taps in ([7, 5, 4, 3], [7, 6, 5, 0], [7, 3, 2, 1]):
+        np.testing.assert_array_equal(LFSR(125, 8, taps).simulate(),
+                                      O.lfsr_sequence(8, 125, taps, 256))
+
+
+@pytest.mark.parametrize("L,R,mode,srs", [(256, 256, "bitrev", True), (64, 256, "bitrev", True),
+                                          (64, 64, "bitrev", True), (16, 16, "counter", True),
+                                          (128, 128, "random", True), (32, 32, "bitrev", False),
+                                          (64, 64, "off", True)])
+def test_prepare_prefix(L, R, mode, srs):
+    from scmp_kernels_amd.sc import tables as TB
+    D = 300
+    cfg = O.make_sobol_simple_config(D, D, 8)
+    ref_full = O.sng_sequences(cfg, "k", 8)
+    got_full = TB.side_sequences(cfg, "k", 8, D, _dev())
+    bits_equal(got_full, ref_full)
+    masks = TB.owen_masks(D, 256, mode)
+    ref_masks = O.owen_masks(D, 256, mode)
+    if masks is None:
+        assert ref_masks is None
+    else:
+        np.testing.assert_array_equal(masks, ref_masks)
+    got = TB.prepare(got_full, 8, L, R, masks, srs)
+    bits_equal(got, O.prepare_prefix(ref_full, 8, L, R, mode, srs))
+
+
+def test_scrambled_config_sequences():
+    from scmp_kernels_amd.sc import tables as TB
+    from scmp_kernels_amd.sc.config_helpers import make_sobol_custom_seed_config
+    import random
+    random.seed(5)
+    cfg = make_sobol_custom_seed_config(40, 40, 8, use_scrambling=True)
+    for side in ("q", "k"):
+        bits_equal(TB.side_sequences(cfg, side, 8, 40, _dev()), O.sng_sequences(cfg, side, 8))
+    # shared RNG with some elements unscrambled -> identity over sc_prec bits
+    cfg["rng_pool"] = [{"type": "lfsr", "seed": 77, "taps": [7, 5, 4, 3]}]
+    for s in cfg["sng"]["q"] + cfg["sng"]["k"]:
+        s["rng_id"] = 0
+    cfg["sng"]["q"][3]["scramble"] = None
+    for side in ("q", "k"):
+        bits_equal(TB.side_sequences(cfg, side, 8, 40, _dev()), O.sng_sequences(cfg, side, 8))
+
+
+def _lut_counts(tabs, c, L):
+    """count[qa_row, qb_row] = sum_{j' < jtab[|qa|]} lut[qb_row][j'] from the HIP tables."""
+    JP = tabs.JP
+    lut = tabs.lut[c].cpu().numpy().astype(np.int64)        # (256, JP) interleaved bytes
+    U = JP // 4
+    jp = np.arange(JP)
+    byte_of = 4 * (jp % U) + jp // U                          # logical j' -> byte offset
+    logical = lut[:, byte_of]                                 # (256, JP) in j' order
+    cum = np.concatenate([np.zeros((256, 1), np.int64), np.cumsum(logical, axis=1)], axis=1)
+    return cum, tabs.jtab[c].cpu().numpy().astype(np.int64)
+
+
+@pytest.mark.parametrize("L,R,bipolar,p", [(256, 256, True, 8), (128, 128, True, 8),
+                                           (64, 64, False, 8), (16, 16, False, 8),
+                                           (256, 256, False, 8), (64, 256, True, 8),
+                                           (64, 64, True, 6), (32, 32, True, 8)])
+def test_stream_tables_match_reference_tables(L, R, bipolar, p):
+    """sum_{j'<j(q_a)} lut[q_b][j'] == C[K[beta(q_a)], beta(q_b)] for every class, q_a, q_b."""
+    from scmp_kernels_amd.sc import tables as TB
+    from scmp_kernels_amd.sc.config_helpers import make_sobol_simple_config
+    D = 260
+    TB.clear()
+    tabs = TB.get_tables(None, ("t", D, p), lambda: make_sobol_simple_config(D, D, p), p, L, R,
+                         bipolar, D, _dev())
+    ref = O.Tables(O.make_sobol_simple_config(D, D, p), p, L, R)
+    Q = 2 ** (p - 1) - 1 if bipolar else 2 ** p - 1
+    qmax = Q + 1 if bipolar else Q
+    beta = TB.beta_of_q(np.arange(qmax + 1), Q, R)
+    reps = {}
+    for d in range(D):
+        reps.setdefault(int(tabs.class_of[d]), d)
+    for c, d in reps.items():
+        cum, jtab = _lut_counts(tabs, c, L)
+        td = ref.tab_of[d]
+        K, C = ref.K[td], ref.C[td]
+        for qa in range(qmax + 1):
+            ka = K[beta[qa]]
+            j = jtab[qa]
+            for qb in range(-(Q + 1) if bipolar else 0, Q + 1):
+                row = qb & 0xff
+                want = C[ka, beta[abs(qb)]] * (-1 if qb < 0 else 1)
+                assert cum[row, j] == want, (c, qa, qb, cum[row, j], want)
+
+
+# -------------------------------------------------------------------------------------
+# quantizers
+# -------------------------------------------------------------------------------------
+
+def _qx(seed=0, rows=37, cols=131):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    x[0, :6] = [0.0, 0.5, -0.5, 1.5, -2.5, 1e-7]
+    x[1] = 0.0
+    x[2] *= 1e-6
+    return x
+
+
+def test_quant_fused_perrow():
+    from scmp_kernels_amd.quant import fused_quantize_bipolar_perrow
+    x = _qx(1)
+    for R in (256, 64, 16):
+        b, s, sc = fused_quantize_bipolar_perrow(T(x), 8, rng_levels=R)
+        rb, rs, rsc = O.quant_fused_perrow_bipolar(x, 8, R)
+        bits_equal(b, rb); bits_equal(s, rs); bits_equal(sc, rsc)
+
+
+def test_quant_fused_tensor_and_unipolar():
+    from scmp_kernels_amd.quant import fused_quantize_bipolar, fused_quantize_unipolar
+    x = _qx(2)
+    am = float(np.abs(x).max())
+    b, s, sc = fused_quantize_bipolar(T(x), am, 8)
+    rb, rs, rsc = O.quant_fused_bipolar(x, am, 8, 256)
+    bits_equal(b, rb); bits_equal(s, rs); assert sc == rsc
+    for R in (256, 64):
+        b, sc, zp, rsum = fused_quantize_unipolar(T(x), float(x.max()), float(x.min()), 8,
+                                                  compute_sum=True, rng_levels=R)
+        rb, rsc, rzp, rrs = O.quant_fused_unipolar(x, float(x.max()), float(x.min()), 8, R)
+        bits_equal(b, rb); bits_equal(rsum, rrs); assert (sc, zp) == (rsc, rzp)
+
+
+@pytest.mark.parametrize("G", [1, 4, 5, 100])
+def test_quant_grouped(G):
+    from scmp_kernels_amd.quant import _grouped_symmetric_quant, _grouped_asymmetric_quant
+    x = _qx(3)
+    s, xi, sg = _grouped_symmetric_quant(T(x), G, 127)
+    rs, rxi, rsg = O.grouped_sym(x, G, 127)
+    bits_equal(s, rs); bits_equal(xi, rxi); bits_equal(sg, rsg)
+    s, zp, xi = _grouped_asymmetric_quant(T(x), G, 255)
+    rs, rzp, rxi = O.grouped_asym(x, G, 255)
+    bits_equal(s, rs); bits_equal(zp, rzp); bits_equal(xi, rxi)
+
+
+def test_quant_grouped_batched():
+    from scmp_kernels_amd.quant import _grouped_symmetric_quant_batched
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((3, 7, 19)).astype(np.float32)
+    for G in (1, 7, 10):
+        s, xi, sg = _grouped_symmetric_quant_batched(T(x), G, 127)
+        rs, rxi, rsg = O.grouped_sym_batched(x, G, 127)
+        bits_equal(s, rs); bits_equal(xi, rxi); bits_equal(sg, rsg)
+    with pytest.raises(NotImplementedError):
+        _grouped_symmetric_quant_batched(T(x), 3, 127)
+
+
+# -------------------------------------------------------------------------------------
+# the SC GEMM: integer accumulator against the oracle
+# -------------------------------------------------------------------------------------
+
+def _int_accum_gpu(a, b, *, L, R, bipolar, group=1, impl=0, tile=0, D=None):
+    """I[n, m] through the product kernels (quantizer codes + scmp_sc_gemm EPI_INT)."""
+    from scmp_kernels_amd import _lib
+    from scmp_kernels_amd.sc import kernels as K
+    dev = _dev()
+    A, B = T(a), T(b)
+    N, D = a.shape
+    M = b.shape[0]
+    tabs = K._get_tables(None, 8, L, R, bipolar, D, dev)
+    ca, cb = K._codes(N, D, dev), K._codes(M, D, dev)
+    var = _lib.Q_GROUP_SYM if bipolar else _lib.Q_GROUP_ASYM
+    Q = 127 if bipolar else 255
+    w1 = K.quantize(A, var, Q, R, group=group, code=ca, code_kind=_lib.CODE_THERMO,
+                    jtab=tabs.jtab, col_class=tabs.d_class)
+    w2 = K.quantize(B, var, Q, R, group=group, code=cb, code_kind=_lib.CODE_Q)
+    I = torch.empty((N, M), dtype=torch.int32, device=dev)
+    epi = _lib.Epilogue()
+    epi.kind = _lib.EPI_INT
+    K.sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, iout=I, impl=impl, tile=tile)
+    torch.cuda.synchronize()
+    del w1, w2
+    return I.cpu().numpy()
+
+
+def _int_accum_ref(a, b, *, L, R, bipolar, group=1):
+    D = a.shape[1]
+    tabs = O.Tables(O.make_sobol_simple_config(D, D, 8), 8, L, R)
+    if bipolar:
+        sa, qa, sga = O.grouped_sym(a, group, 127)
+        sb, qb, sgb = O.grouped_sym(b, group, 127)
+        return O.sc_accum(O.beta_div(qa, 127, R), sga, O.beta_div(qb, 127, R), sgb, tabs)
+    sa, za, qa = O.grouped_asym(a, group, 255)
+    sb, zb, qb = O.grouped_asym(b, group, 255)
+    return O.sc_accum(O.beta_div(qa, 255, R, False), None, O.beta_div(qb, 255, R, False), None,
+                      tabs)
+
+
+GEMM_CASES = [
+    # (N, M, D, L, R, bipolar)    JP: 128 / 128 / 64 / 16 / 256 / 32
+    (70, 45, 96, 256, 256, True),
+    (257, 300, 200, 128, 128, True),
+    (33, 97, 77, 64, 64, False),
+    (40, 31, 50, 16, 16, False),
+    (65, 66, 129, 256, 256, False),
+    (31, 129, 64, 32, 32, True),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_CASES)
+@pytest.mark.parametrize("impl,tile", [(0, 0), (0, 1), (1, 0)])
+def test_gemm_int_accumulator(case, impl, tile):
+    N, M, D, L, R, bip = case
+    rng = np.random.default_rng(N * 7 + M)
+    a = rng.standard_normal((N, D)).astype(np.float32)
+    b = rng.standard_normal((M, D)).astype(np.float32)
+    a[3] = 0.0                                     # an all-zero row
+    got = _int_accum_gpu(a, b, L=L, R=R, bipolar=bip, impl=impl, tile=tile)
+    ref = _int_accum_ref(a, b, L=L, R=R, bipolar=bip)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_gemm_extremes():
+    """Saturated operands: every code at +-Q (full-length Sobol: count = L per d)."""
+    N, M, D = 64, 64, 48
+    a = np.ones((N, D), np.float32)
+    a[::2] *= -1
+    b = np.ones((M, D), np.float32)
+    got = _int_accum_gpu(a, b, L=256, R=256, bipolar=True)
+    ref = _int_accum_ref(a, b, L=256, R=256, bipolar=True)
+    np.testing.assert_array_equal(got, ref)
+    assert abs(int(got[0, 0])) == 256 * D
+
+
+# -------------------------------------------------------------------------------------
+# sc_matmul end to end
+# -------------------------------------------------------------------------------------
+
+with open(os.path.join(GOLD, "cases.json")) as f:
+    _CASES = json.load(f)
+GOLDEN_MATMUL = sorted(k for k, v in _CASES.items() if v["kind"] == "sc_matmul")
+
+
+@pytest.mark.parametrize("name", GOLDEN_MATMUL)
+def test_sc_matmul_golden(name, monkeypatch):
+    from scmp_kernels_amd import sc_matmul
+    from scmp_kernels_amd.sc import clear_rng_cache
+    meta = _CASES[name]
+    with np.load(os.path.join(GOLD, f"{name}.npz"), allow_pickle=False) as z:
+        z = {k: z[k] for k in z.files}
+    for k, v in meta["env"].items():
+        monkeypatch.setenv(k, v)
+    clear_rng_cache()
+    kw = dict(meta["kwargs"])
+    if "smooth" in z:
+        kw["smooth_scales"] = T(z["smooth"])
+    y = sc_matmul(T(z["a"]), T(z["b"]), **kw)
+    clear_rng_cache()
+    bits_equal(y, z["y"])
+
+
+RANDOM_CASES = [
+    ("per_row", dict(mode="bipolar"), (129, 67, 300)),
+    ("per_row", dict(mode="unipolar", group_a=4, group_b=4), (130, 70, 96)),
+    ("per_row", dict(mode="unipolar", group_a=4, group_b=4, stoc_len=64, rng_levels=64),
+     (97, 61, 200)),
+    ("per_row", dict(mode="unipolar", group_a=4, group_b=3, stoc_len=16, rng_levels=16),
+     (50, 40, 64)),
+    ("per_row", dict(mode="bipolar", chunk_d=72), (300, 65, 3 * 72 + 48)),
+    ("per_row", dict(mode="bipolar", halve_bipolar_stoc_len=True), (64, 64, 128)),
+    ("per_tensor", dict(mode="bipolar"), (32, 64, 256)),
+    ("per_tensor", dict(mode="unipolar"), (40, 33, 100)),
+]
+
+
+@pytest.mark.parametrize("gran,kw,shape", RANDOM_CASES)
+def test_sc_matmul_vs_oracle(gran, kw, shape):
+    from scmp_kernels_amd import sc_matmul
+    N, M, D = shape
+    rng = np.random.default_rng(N + M + D)
+    a = rng.standard_normal((N, D)).astype(np.float32)
+    b = (rng.standard_normal((M, D)) * 0.05).astype(np.float32)
+    y = sc_matmul(T(a), T(b), gran, **kw)
+    bits_equal(y, O.sc_matmul(a, b, gran, **kw))
+
+
+@pytest.mark.parametrize("shape", [(6, 197, 64, 197), (4, 197, 197, 64), (3, 300, 20, 33)])
+def test_per_head_vs_oracle(shape):
+    from scmp_kernels_amd import sc_matmul
+    BH, N, D, M = shape
+    rng = np.random.default_rng(sum(shape))
+    q = rng.standard_normal((BH, N, D)).astype(np.float32)
+    k = rng.standard_normal((BH, M, D)).astype(np.float32)
+    y = sc_matmul(T(q), T(k), "per_head")
+    bits_equal(y, O.sc_matmul(q, k, "per_head"))
+
+
+def test_per_row_3d_vs_oracle():
+    from scmp_kernels_amd import sc_matmul
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((5, 40, 64)).astype(np.float32)
+    b = rng.standard_normal((5, 33, 64)).astype(np.float32)
+    bits_equal(sc_matmul(T(a), T(b), "per_row"), O.sc_matmul(a, b, "per_row"))
+    bits_equal(sc_matmul(T(a), T(b), "per_tensor"), O.sc_matmul(a, b, "per_tensor"))
