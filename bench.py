@@ -1,0 +1,255 @@
+"""Benchmark of the SC matmul hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5]
+                    [--impl mfma|valu] [--no-cpu]
+
+Default workload (BASELINE.json's metric, configuration 2): one
+``sc_matmul(a, b, "per_row", sc_prec=8, stoc_len=256, smooth_scales=s)`` with
+a (4096, 4096) ~ N(0,1) with 1% of channels x20, b (11008, 4096) ~ N(0, 0.02^2),
+s = compute_smooth_scales(accumulate_act_scales(a), b, 0.5). Inputs are generated on the
+host with numpy's seeded PCG64 and are resident in HBM before timing. A step is one full
+sc_matmul call (quantize a, quantize b, SC GEMM, epilogue).
+
+Printed: one JSON line. ``value`` is SC bit-ops/s = N*M*D*stoc_len / step time (the
+reference's unit of work; the MFMA kernel executes its own, smaller op count, reported in
+``roofline``). ``roofline`` times the dominant kernel (the MFMA SC GEMM) with HIP events on
+the stream it runs on. ``cpu_baseline`` times the CPU oracle on a row sample of the same
+workload and checks those rows bit-exactly against the GPU result.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
+VALU_PEAK_TOPS = 256 * 4 * 16 * 2.4e9 / 1e12 * 1.0  # 64 lane-ops/clk/CU at 2.4 GHz
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_cfg2(seed_a=1, seed_b=2, seed_ch=3):
+    N, M, D = 4096, 11008, 4096
+    ra = np.random.default_rng(seed_a)
+    a = ra.standard_normal((N, D), dtype=np.float32)
+    ch = np.random.default_rng(seed_ch).choice(D, size=D // 100, replace=False)
+    a[:, ch] *= 20.0
+    b = (np.random.default_rng(seed_b).standard_normal((M, D), dtype=np.float32) * 0.02)
+    return a, b.astype(np.float32)
+
+
+def time_steps(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps, out
+
+
+def gemm_event_time(run, reps):
+    """Average duration of one launch of the dominant kernel, HIP events on the current
+    stream (the stream the library launches on)."""
+    import torch
+    s = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    run()
+    torch.cuda.synchronize()
+    for e0, e1 in ev:
+        e0.record(s)
+        run()
+        e1.record(s)
+    torch.cuda.synchronize()
+    ms = [e0.elapsed_time(e1) for e0, e1 in ev]
+    return float(np.mean(ms)), float(np.min(ms))
+
+
+def bench_cfg2(args):
+    import torch
+    from scmp_kernels_amd import sc_matmul, _lib
+    from scmp_kernels_amd.sc import kernels as K
+    from scmp_kernels_amd.quant import accumulate_act_scales, compute_smooth_scales
+
+    dev = torch.device("cuda", 0)
+    t0 = time.perf_counter()
+    a_h, b_h = make_cfg2()
+    a = torch.from_numpy(a_h).to(dev)
+    b = torch.from_numpy(b_h).to(dev)
+    s = compute_smooth_scales(accumulate_act_scales(a), b, alpha=0.5)
+    log(f"inputs ready in {time.perf_counter() - t0:.1f}s")
+    N, D = a.shape
+    M = b.shape[0]
+    L = 256
+    os.environ["SCMP_GEMM_IMPL"] = args.impl
+
+    def step():
+        return sc_matmul(a, b, "per_row", sc_prec=8, stoc_len=L, smooth_scales=s)
+
+    t_step, y = time_steps(step, args.steps, args.warmup)
+    log(f"sc_matmul step: {t_step * 1e3:.3f} ms")
+
+    # dominant kernel alone: the SC GEMM on pre-quantized codes, int32 output
+    tabs = K._get_tables(None, 8, L, 256, True, D, dev)
+    ca, cb = K._codes(N, D, dev), K._codes(M, D, dev)
+    K.quantize(a, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_DIV, code=ca,
+               code_kind=_lib.CODE_THERMO, jtab=tabs.jtab)
+    K.quantize(b, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_MUL, code=cb,
+               code_kind=_lib.CODE_Q)
+    I = torch.empty((N, M), dtype=torch.int32, device=dev)
+    epi = _lib.Epilogue()
+    epi.kind = _lib.EPI_INT
+    impl = _lib.GEMM_VALU if args.impl == "valu" else _lib.GEMM_MFMA
+
+    def gemm():
+        K.sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, iout=I, impl=impl)
+
+    g_avg, g_min = gemm_event_time(gemm, max(3, args.steps))
+    log(f"SC GEMM kernel: avg {g_avg:.3f} ms, min {g_min:.3f} ms (JP={tabs.JP})")
+    B = N * M * D * L
+    if impl == _lib.GEMM_MFMA:
+        ops = 2.0 * N * M * D * tabs.JP          # int8 MACs the kernel issues, x2
+        peak, bound = MFMA_INT8_PEAK_TOPS, "mfma"
+        kname = "sc_gemm_mfma_kernel"
+    else:
+        ops = float(N * M * D * (tabs.JP // 32) * 2 * 2)  # (AND + BCNT) x 2 planes per word
+        peak, bound = VALU_PEAK_TOPS, "valu"
+        kname = "sc_gemm_valu_kernel"
+    achieved = ops / (g_avg * 1e-3) / 1e12
+    roof = {
+        "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": "TOP/s",
+        "frac": round(achieved / peak, 4), "traffic": None,
+        "kernel": kname, "avg_ms": round(g_avg, 4), "ops_per_launch": ops,
+        "effective_sc_bitops_per_s": B / (g_avg * 1e-3),
+    }
+    tp = os.path.join(ROOT, "profiles", "cfg2_gemm_traffic.json")
+    if os.path.exists(tp):
+        with open(tp) as f:
+            roof["traffic"] = json.load(f).get("traffic_bytes")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(a_h, b_h, s.cpu().numpy(), y, rows=args.cpu_rows)
+    return {
+        "metric": "ms & SC bit-ops/s per sc_matmul (M=4096,N=11008,D=4096, per_row, sc_prec=8)",
+        "value": B / t_step,
+        "unit": "SC bit-ops/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic (numpy PCG64 seeds 1,2,3)",
+        "config": {"workload": "cfg2: LLM linear per_row bipolar + SmoothQuant",
+                   "a": [N, D], "b": [M, D], "sc_prec": 8, "stoc_len": L,
+                   "granularity": "per_row", "impl": args.impl},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+
+
+def profile_gemm(args):
+    """One launch of the dominant kernel on the cfg2 operands, then one device copy of a
+    known size (8 * 2^27 bytes each way) whose FETCH_SIZE / WRITE_SIZE counter values scale
+    the GEMM's counters to bytes. Used under rocprofv3 --pmc."""
+    import torch
+    from scmp_kernels_amd import _lib
+    from scmp_kernels_amd.sc import kernels as K
+    from scmp_kernels_amd.quant import accumulate_act_scales, compute_smooth_scales
+    dev = torch.device("cuda", 0)
+    a_h, b_h = make_cfg2()
+    a = torch.from_numpy(a_h).to(dev)
+    b = torch.from_numpy(b_h).to(dev)
+    s = compute_smooth_scales(accumulate_act_scales(a), b, alpha=0.5)
+    N, D = a.shape
+    M = b.shape[0]
+    tabs = K._get_tables(None, 8, 256, 256, True, D, dev)
+    ca, cb = K._codes(N, D, dev), K._codes(M, D, dev)
+    K.quantize(a, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_DIV, code=ca,
+               code_kind=_lib.CODE_THERMO, jtab=tabs.jtab)
+    K.quantize(b, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_MUL, code=cb,
+               code_kind=_lib.CODE_Q)
+    I = torch.empty((N, M), dtype=torch.int32, device=dev)
+    epi = _lib.Epilogue()
+    epi.kind = _lib.EPI_INT
+    impl = _lib.GEMM_VALU if args.impl == "valu" else _lib.GEMM_MFMA
+    torch.cuda.synchronize()
+    K.sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, iout=I, impl=impl,
+              tile=args.tile)
+    torch.cuda.synchronize()
+    src = torch.ones(2 ** 28, dtype=torch.int32, device=dev)     # 1 GiB
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log("profile_gemm: one GEMM launch, then a 1 GiB device copy")
+
+
+def cpu_baseline(a_h, b_h, s_h, y_gpu, rows):
+    """The CPU oracle (C, OpenMP) on `rows` rows of a against all of b: same per-row work
+    as the GPU step, scaled to bit-ops/s. Also a bit-exact check of those rows."""
+    import torch
+    from oracle import sc_oracle as O
+    nthreads = min(16, os.cpu_count() or 1)
+    idx = np.linspace(0, a_h.shape[0] - 1, rows).astype(np.int64)
+    a_s = a_h[idx]
+    O.lib()
+    t0 = time.perf_counter()
+    y_ref = O.sc_matmul(a_s, b_h, "per_row", sc_prec=8, stoc_len=256, smooth_scales=s_h,
+                        ctx=O.Ctx(nthreads=nthreads))
+    dt = time.perf_counter() - t0
+    got = y_gpu[torch.from_numpy(idx).to(y_gpu.device)].cpu().numpy()
+    exact = bool(np.array_equal(got.view(np.uint32), y_ref.view(np.uint32)))
+    B = rows * b_h.shape[0] * a_h.shape[1] * 256
+    log(f"cpu oracle: {rows} rows in {dt:.1f}s on {nthreads} threads; bit-exact={exact}")
+    return {"value": B / dt, "unit": "SC bit-ops/s", "cores": nthreads, "kind": "port",
+            "sample": f"{rows} of 4096 rows of a (evenly spaced) x all 11008 rows of b, "
+                      f"D=4096, full pipeline (smoothing, quantizers, table accumulator, "
+                      f"epilogue); {dt:.1f} s",
+            "sample_bit_exact_vs_gpu": exact}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg2")
+    ap.add_argument("--impl", default="mfma", choices=["mfma", "valu"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=1024)
+    ap.add_argument("--mode", default="step", choices=["step", "gemm"],
+                    help="step: the benchmark (default); gemm: one dominant-kernel launch "
+                         "plus a 1 GiB copy, for counter collection")
+    ap.add_argument("--tile", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build runs the SC matmul on a single "
+              f"MI355X); --gpus {args.gpus} is not supported.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    if args.config != "cfg2":
+        print(f"unknown --config {args.config}", file=sys.stderr)
+        sys.exit(2)
+    if args.mode == "gemm":
+        profile_gemm(args)
+        return
+    res = bench_cfg2(args)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

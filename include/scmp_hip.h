@@ -180,8 +180,10 @@ typedef struct scmp_epilogue {
     float dfloat;              /* ZP_ROWCOL: D as fp32 */
 } scmp_epilogue;
 
-#define SCMP_GEMM_MFMA 0       /* int8 MFMA (v_mfma_i32_32x32x32_i8), default */
+#define SCMP_GEMM_MFMA 0       /* int8 MFMA (v_mfma_i32_32x32x32_i8) */
 #define SCMP_GEMM_VALU 1       /* bit-packed AND + v_bcnt (comparison kernel) */
+#define SCMP_GEMM_MFMA_FP4 2   /* FP4 (e2m1) MFMA (v_mfma_f32_32x32x64_f8f6f4); lut is the
+                                  table of scmp_build_fp4_lut */
 
 typedef struct scmp_gemm_args {
     const uint8_t *ca;         /* A codes (THERMO), rows padded to a multiple of 256 */
@@ -204,6 +206,13 @@ typedef struct scmp_gemm_args {
 } scmp_gemm_args;
 
 int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream);
+
+/* FP4 (e2m1) form of a stream table for SCMP_GEMM_MFMA_FP4: JPF = max(JP, 32) nibbles per
+ * row (JPF / 2 bytes), dword u nibble b holds interval j' = (JPF/8)*b + u. Counts that e2m1
+ * cannot represent exactly (anything but 0, 1, 2, 3, 4, 6) set *bad to 1; the table is then
+ * unusable and the int8 kernel must be used. */
+int scmp_build_fp4_lut(const int8_t *lut, int nclass, int JP, uint8_t *lut4, int32_t *bad,
+                       hipStream_t stream);
 
 /* Bit planes of a stream table for SCMP_GEMM_VALU: bitlut[c][row][plane][w] bit u of
  * word w is bit `plane` of |lut[c][row][j']| for j' = 32w + u (logical interval order). */

@@ -26,7 +26,7 @@ SCMP_OK = 0
 SMOOTH_NONE, SMOOTH_DIV, SMOOTH_MUL = 0, 1, 2
 CODE_NONE, CODE_THERMO, CODE_Q = 0, 1, 2
 EPI_INT, EPI_ROWCOL, EPI_SCALAR, EPI_HEAD, EPI_ZP_ROWCOL, EPI_ZP_SCALAR = range(6)
-GEMM_MFMA, GEMM_VALU = 0, 1
+GEMM_MFMA, GEMM_VALU, GEMM_MFMA_FP4 = 0, 1, 2
 
 
 class QuantArgs(ctypes.Structure):
@@ -68,6 +68,7 @@ EXPORTS = [
     "scmp_abi_version", "scmp_last_error", "scmp_rng_sobol", "scmp_rng_lfsr",
     "scmp_rng_expand", "scmp_rng_prepare", "scmp_build_stream_tables",
     "scmp_quant_workspace_bytes", "scmp_quantize", "scmp_sc_gemm", "scmp_build_bitlut",
+    "scmp_build_fp4_lut",
 ]
 
 _lib = None
@@ -101,6 +102,7 @@ def load(path: str = LIB_PATH):
         lib.scmp_quantize.argtypes = [ctypes.POINTER(QuantArgs), c_vp]
         lib.scmp_sc_gemm.argtypes = [ctypes.POINTER(GemmArgs), c_vp]
         lib.scmp_build_bitlut.argtypes = [c_vp, c_int, c_int, c_vp, c_vp]
+        lib.scmp_build_fp4_lut.argtypes = [c_vp, c_int, c_int, c_vp, c_vp, c_vp]
         for name in EXPORTS:
             getattr(lib, name).restype = getattr(lib, name).restype or c_int
         lib.scmp_last_error.restype = ctypes.c_char_p

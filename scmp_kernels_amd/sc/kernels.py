@@ -134,9 +134,12 @@ def quantize(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, *, grou
     return ws  # keep the workspace alive until the stream has consumed it
 
 
-def _gemm_impl() -> int:
-    return _lib.GEMM_VALU if os.environ.get("SCMP_GEMM_IMPL", "mfma").lower() == "valu" \
-        else _lib.GEMM_MFMA
+def _gemm_impl() -> Optional[int]:
+    """SCMP_GEMM_IMPL = fp4 | int8 | valu selects the SC GEMM kernel; unset: FP4 MFMA
+    when the stream table fits e2m1, else int8 MFMA."""
+    v = os.environ.get("SCMP_GEMM_IMPL", "").lower()
+    return {"valu": _lib.GEMM_VALU, "int8": _lib.GEMM_MFMA, "mfma": _lib.GEMM_MFMA,
+            "fp4": _lib.GEMM_MFMA_FP4}.get(v)
 
 
 def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.Epilogue",
@@ -150,7 +153,18 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
     g.bsb = cb.shape[-2] * cb.shape[-1] if cb.dim() == 3 else 0
     g.N, g.M, g.D, g.batch = N, M, D, batch
     g.bipolar, g.JP = 1 if tabs.bipolar else 0, tabs.JP
-    g.lut = tabs.lut.data_ptr()
+    dev = ca.device
+    stream = _lib.stream_of(dev)
+    if impl is None:
+        impl = _gemm_impl()
+    if impl is None and D > 65536:
+        impl = _lib.GEMM_MFMA  # the FP4 kernel's fp32 accumulator is exact up to 2^24
+    if impl is None or impl == _lib.GEMM_MFMA_FP4:
+        l4 = tabs.lut4(stream)
+        if l4 is None and impl == _lib.GEMM_MFMA_FP4:
+            raise ValueError("sc_matmul: the stream table has counts FP4 cannot represent")
+        impl = _lib.GEMM_MFMA_FP4 if l4 is not None else _lib.GEMM_MFMA
+    g.lut = tabs.lut4(stream).data_ptr() if impl == _lib.GEMM_MFMA_FP4 else tabs.lut.data_ptr()
     dc = d_class if d_class is not None else tabs.d_class
     g.d_class = _lib.ptr(dc)
     g.chunk = chunk
@@ -158,12 +172,11 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
     g.y, g.iout = _lib.ptr(y), _lib.ptr(iout)
     g.ldy = ldy if ldy is not None else M
     g.bsy = bsy
-    g.impl = _gemm_impl() if impl is None else impl
+    g.impl = impl
     g.tile = int(os.environ.get("SCMP_GEMM_TILE", "0")) if tile is None else tile
-    dev = ca.device
     if g.impl == _lib.GEMM_VALU:
-        g.bitlut = tabs.bitlut(_lib.stream_of(dev)).data_ptr()
-    _lib.check(_lib.load().scmp_sc_gemm(g, _lib.stream_of(dev)), "scmp_sc_gemm")
+        g.bitlut = tabs.bitlut(stream).data_ptr()
+    _lib.check(_lib.load().scmp_sc_gemm(g, stream), "scmp_sc_gemm")
 
 
 def _codes(rows: int, D: int, device, batch: int = 0) -> torch.Tensor:
@@ -312,8 +325,9 @@ def _sc_matmul_per_row_mlp(a, b, mode="bipolar", sc_prec=8, config=None, group_a
     epi.kind, epi.c = _lib.EPI_ROWCOL, _inner_scale(Q, stoc_len)
     epi.sa, epi.sb = sa.data_ptr(), sb.data_ptr()
     epi.sa_chunk_stride, epi.sb_chunk_stride = N, M
+    impl = _gemm_impl()
     sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, y=y, chunk=chunk_d,
-            d_class=d_class, impl=_lib.GEMM_MFMA)
+            d_class=d_class, impl=None if impl == _lib.GEMM_VALU else impl)
     del w1, w2
     return y.to(home) if home is not None else y
 

@@ -113,6 +113,23 @@ class StreamTables:
     ra: torch.Tensor             # prepared A-side sequences (D, L) int32
     rb: torch.Tensor             # prepared B-side sequences (D, L) int32
     _bitlut: Optional[torch.Tensor] = None
+    _lut4: Optional[torch.Tensor] = None
+    _fp4_ok: Optional[bool] = None
+
+    def lut4(self, stream) -> Optional[torch.Tensor]:
+        """FP4 (e2m1) form of the table, or None when some count is not representable
+        (then only the int8 kernel applies). Built on first use."""
+        if self._fp4_ok is None:
+            JPF = max(self.JP, 32)
+            l4 = torch.empty((self.nclass, 256, JPF // 2), dtype=torch.uint8,
+                             device=self.lut.device)
+            bad = torch.zeros(1, dtype=torch.int32, device=self.lut.device)
+            _lib.check(_lib.load().scmp_build_fp4_lut(
+                self.lut.data_ptr(), self.nclass, self.JP, l4.data_ptr(), bad.data_ptr(),
+                stream), "scmp_build_fp4_lut")
+            self._fp4_ok = int(bad.item()) == 0
+            self._lut4 = l4 if self._fp4_ok else None
+        return self._lut4
 
     def bitlut(self, stream) -> torch.Tensor:
         """Bit planes for the VALU comparison kernel (built on first use)."""

@@ -253,8 +253,12 @@ GEMM_CASES = [
 ]
 
 
+# (impl, tile): int8 MFMA presets 0-4, VALU popcount, FP4 MFMA presets 0-1
+KERNELS = [(0, 0), (0, 1), (0, 2), (0, 3), (0, 4), (1, 0), (2, 0), (2, 1)]
+
+
 @pytest.mark.parametrize("case", GEMM_CASES)
-@pytest.mark.parametrize("impl,tile", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("impl,tile", KERNELS)
 def test_gemm_int_accumulator(case, impl, tile):
     N, M, D, L, R, bip = case
     rng = np.random.default_rng(N * 7 + M)
@@ -272,10 +276,11 @@ def test_gemm_extremes():
     a = np.ones((N, D), np.float32)
     a[::2] *= -1
     b = np.ones((M, D), np.float32)
-    got = _int_accum_gpu(a, b, L=256, R=256, bipolar=True)
     ref = _int_accum_ref(a, b, L=256, R=256, bipolar=True)
-    np.testing.assert_array_equal(got, ref)
-    assert abs(int(got[0, 0])) == 256 * D
+    for impl, tile in KERNELS:
+        got = _int_accum_gpu(a, b, L=256, R=256, bipolar=True, impl=impl, tile=tile)
+        np.testing.assert_array_equal(got, ref)
+        assert abs(int(got[0, 0])) == 256 * D
 
 
 # -------------------------------------------------------------------------------------
