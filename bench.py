@@ -1,7 +1,7 @@
 """Benchmark of the SC matmul hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4|cfg5]
-                    [--impl mfma|valu] [--no-cpu]
+                    [--impl auto|fp4|int8|valu] [--no-cpu]
 
 Default workload (BASELINE.json's metric, configuration 2): one
 ``sc_matmul(a, b, "per_row", sc_prec=8, stoc_len=256, smooth_scales=s)`` with
@@ -12,8 +12,8 @@ sc_matmul call (quantize a, quantize b, SC GEMM, epilogue).
 
 Printed: one JSON line. ``value`` is SC bit-ops/s = N*M*D*stoc_len / step time (the
 reference's unit of work; the MFMA kernel executes its own, smaller op count, reported in
-``roofline``). ``roofline`` times the dominant kernel (the MFMA SC GEMM) with HIP events on
-the stream it runs on. ``cpu_baseline`` times the CPU oracle on a row sample of the same
+``roofline``). ``roofline`` times the dominant kernel (the SC GEMM: FP4 e2m1 MFMA by
+default, int8 MFMA or VALU popcount with --impl) with HIP events on the stream it runs on. ``cpu_baseline`` times the CPU oracle on a row sample of the same
 workload and checks those rows bit-exactly against the GPU result.
 """
 from __future__ import annotations
@@ -30,6 +30,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 MFMA_INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
+MFMA_FP4_PEAK_TFLOPS = 10100.0  # MI355X dense fp4 MFMA, 10.1 PFLOP/s
 VALU_PEAK_TOPS = 256 * 4 * 16 * 2.4e9 / 1e12 * 1.0  # 64 lane-ops/clk/CU at 2.4 GHz
 
 
@@ -77,6 +78,39 @@ def gemm_event_time(run, reps):
     return float(np.mean(ms)), float(np.min(ms))
 
 
+# arithmetic the SC GEMM computes in: every kernel counts integers exactly
+DTYPE = {0: "int8 MFMA (exact int32 counts)", 1: "u32 popcount (exact int32 counts)",
+         2: "e2m1 MFMA (exact integer counts in fp32)"}
+
+
+def resolve_impl(name, tabs):
+    """The kernel id the library runs for --impl `name` (auto follows sc/kernels.py)."""
+    from scmp_kernels_amd import _lib
+    if name == "valu":
+        return _lib.GEMM_VALU
+    if name == "int8":
+        return _lib.GEMM_MFMA
+    has4 = tabs.lut4(_lib.stream_of(tabs.lut.device)) is not None
+    if name == "fp4" and not has4:
+        raise SystemExit("--impl fp4: the stream table has counts e2m1 cannot represent")
+    return _lib.GEMM_MFMA_FP4 if has4 else _lib.GEMM_MFMA
+
+
+def kernel_roofline(impl, N, M, D, JP):
+    """(ops per launch, peak in 1e12/s, unit, bound, kernel name) for the SC GEMM kernel.
+    The MFMA kernels issue one multiply-add per (n, m, d, interval) over the padded interval
+    extent (JP for int8, max(JP, 32) for FP4); the VALU kernel an AND and a popcount per
+    32-interval word and bit plane."""
+    if impl == 2:
+        return (2.0 * N * M * D * max(JP, 32), MFMA_FP4_PEAK_TFLOPS, "TFLOP/s", "mfma",
+                "sc_gemm_fp4_kernel")
+    if impl == 0:
+        return (2.0 * N * M * D * JP, MFMA_INT8_PEAK_TOPS, "TOP/s", "mfma",
+                "sc_gemm_mfma_kernel")
+    return (float(N * M * D * max(1, JP // 32) * 2 * 2), VALU_PEAK_TOPS, "TOP/s", "valu",
+            "sc_gemm_valu_kernel")
+
+
 def bench_cfg2(args):
     import torch
     from scmp_kernels_amd import sc_matmul, _lib
@@ -93,7 +127,8 @@ def bench_cfg2(args):
     N, D = a.shape
     M = b.shape[0]
     L = 256
-    os.environ["SCMP_GEMM_IMPL"] = args.impl
+    if args.impl != "auto":
+        os.environ["SCMP_GEMM_IMPL"] = args.impl
 
     def step():
         return sc_matmul(a, b, "per_row", sc_prec=8, stoc_len=L, smooth_scales=s)
@@ -111,7 +146,7 @@ def bench_cfg2(args):
     I = torch.empty((N, M), dtype=torch.int32, device=dev)
     epi = _lib.Epilogue()
     epi.kind = _lib.EPI_INT
-    impl = _lib.GEMM_VALU if args.impl == "valu" else _lib.GEMM_MFMA
+    impl = resolve_impl(args.impl, tabs)
 
     def gemm():
         K.sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, iout=I, impl=impl)
@@ -119,17 +154,10 @@ def bench_cfg2(args):
     g_avg, g_min = gemm_event_time(gemm, max(3, args.steps))
     log(f"SC GEMM kernel: avg {g_avg:.3f} ms, min {g_min:.3f} ms (JP={tabs.JP})")
     B = N * M * D * L
-    if impl == _lib.GEMM_MFMA:
-        ops = 2.0 * N * M * D * tabs.JP          # int8 MACs the kernel issues, x2
-        peak, bound = MFMA_INT8_PEAK_TOPS, "mfma"
-        kname = "sc_gemm_mfma_kernel"
-    else:
-        ops = float(N * M * D * (tabs.JP // 32) * 2 * 2)  # (AND + BCNT) x 2 planes per word
-        peak, bound = VALU_PEAK_TOPS, "valu"
-        kname = "sc_gemm_valu_kernel"
+    ops, peak, unit, bound, kname = kernel_roofline(impl, N, M, D, tabs.JP)
     achieved = ops / (g_avg * 1e-3) / 1e12
     roof = {
-        "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": "TOP/s",
+        "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
         "frac": round(achieved / peak, 4), "traffic": None,
         "kernel": kname, "avg_ms": round(g_avg, 4), "ops_per_launch": ops,
         "effective_sc_bitops_per_s": B / (g_avg * 1e-3),
@@ -137,7 +165,7 @@ def bench_cfg2(args):
     tp = os.path.join(ROOT, "profiles", "cfg2_gemm_traffic.json")
     if os.path.exists(tp):
         with open(tp) as f:
-            roof["traffic"] = json.load(f).get("traffic_bytes")
+            roof["traffic"] = json.load(f).get(kname, {}).get("traffic_bytes")
 
     cpu = None
     if not args.no_cpu:
@@ -149,10 +177,10 @@ def bench_cfg2(args):
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(t_step * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8", "data": "synthetic (numpy PCG64 seeds 1,2,3)",
+        "dtype": DTYPE[impl], "data": "synthetic (numpy PCG64 seeds 1,2,3)",
         "config": {"workload": "cfg2: LLM linear per_row bipolar + SmoothQuant",
                    "a": [N, D], "b": [M, D], "sc_prec": 8, "stoc_len": L,
-                   "granularity": "per_row", "impl": args.impl},
+                   "granularity": "per_row", "gemm_kernel": kname},
         "roofline": roof,
         "cpu_baseline": cpu,
     }
@@ -182,7 +210,7 @@ def profile_gemm(args):
     I = torch.empty((N, M), dtype=torch.int32, device=dev)
     epi = _lib.Epilogue()
     epi.kind = _lib.EPI_INT
-    impl = _lib.GEMM_VALU if args.impl == "valu" else _lib.GEMM_MFMA
+    impl = resolve_impl(args.impl, tabs)
     torch.cuda.synchronize()
     K.sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, iout=I, impl=impl,
               tile=args.tile)
@@ -225,7 +253,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg2")
-    ap.add_argument("--impl", default="mfma", choices=["mfma", "valu"])
+    ap.add_argument("--impl", default="auto", choices=["auto", "fp4", "int8", "valu"],
+                    help="SC GEMM kernel; auto = the library default (FP4 MFMA when the "
+                         "stream table fits e2m1, else int8 MFMA)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--mode", default="step", choices=["step", "gemm"],

@@ -200,9 +200,11 @@ typedef struct scmp_gemm_args {
     float *y;                  /* fp32 output, row stride ldy, batch stride bsy (elements) */
     int32_t *iout;             /* int32 output for SCMP_EPI_INT */
     int64_t ldy, bsy;
-    int impl;                  /* SCMP_GEMM_MFMA or SCMP_GEMM_VALU */
+    int impl;                  /* SCMP_GEMM_MFMA, SCMP_GEMM_VALU or SCMP_GEMM_MFMA_FP4 */
     const uint32_t *bitlut;    /* VALU only: nclass x 256 x 2 x (JP/32) bit planes */
     int tile;                  /* MFMA tile preset (0 = default) */
+    int nclass;                /* tables in lut; with d_class the FP4 kernel stages them in
+                                  LDS when they fit (0: read them from global memory) */
 } scmp_gemm_args;
 
 int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream);

@@ -60,7 +60,7 @@ class GemmArgs(ctypes.Structure):
         ("bsb", c_i64), ("N", c_i64), ("M", c_i64), ("D", c_i64), ("batch", c_i64),
         ("bipolar", c_int), ("JP", c_int), ("lut", c_vp), ("d_class", c_vp), ("chunk", c_i64),
         ("epi", Epilogue), ("y", c_vp), ("iout", c_vp), ("ldy", c_i64), ("bsy", c_i64),
-        ("impl", c_int), ("bitlut", c_vp), ("tile", c_int),
+        ("impl", c_int), ("bitlut", c_vp), ("tile", c_int), ("nclass", c_int),
     ]
 
 

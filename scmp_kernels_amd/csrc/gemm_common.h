@@ -27,6 +27,7 @@ struct GemmP {
     int32_t *iout;
     int64_t ldy, bsy;
     int tilesA;
+    int nclass;
 };
 
 int run_epilogue(const int32_t *iin, float *y, int64_t N, int64_t M, int64_t batch,

@@ -518,6 +518,7 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     // epilogue pass then converts it in place)
     P.iout = a.epi.kind == SCMP_EPI_INT ? a.iout : (int32_t *)a.y;
     P.tilesA = 0;
+    P.nclass = a.nclass;
     const bool perclass = a.d_class != nullptr;
     int rc;
     if (a.impl == SCMP_GEMM_MFMA_FP4)

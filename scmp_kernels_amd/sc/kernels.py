@@ -167,6 +167,7 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
     g.lut = tabs.lut4(stream).data_ptr() if impl == _lib.GEMM_MFMA_FP4 else tabs.lut.data_ptr()
     dc = d_class if d_class is not None else tabs.d_class
     g.d_class = _lib.ptr(dc)
+    g.nclass = tabs.nclass
     g.chunk = chunk
     g.epi = epi
     g.y, g.iout = _lib.ptr(y), _lib.ptr(iout)
