@@ -30,9 +30,53 @@ struct GemmP {
     int nclass;
 };
 
+// fp32 epilogue of one output element (row n of A, row m of B, batch index) from its
+// exact integer accumulator I, in the operation order of the reference path that the
+// kind stands for. One IEEE rounding per operation (no contraction).
+__device__ __forceinline__ float epilogue_value(const scmp_epilogue &E, float I, int64_t n,
+                                                int64_t m, int64_t batch) {
+    switch (E.kind) {
+    case SCMP_EPI_ROWCOL: {
+        // fl(fl(I*c) * fl(sa*sb)): sc/kernels.py:248 then :1707 / :1271 / :1894
+        const float raw = __fmul_rn(I, E.c);
+        const float s = __fmul_rn(E.sa[batch * E.sa_batch_stride + n],
+                                  E.sb[batch * E.sb_batch_stride + m]);
+        return __fmul_rn(raw, s);
+    }
+    case SCMP_EPI_SCALAR:  // sc/kernels.py:1204 (the scale product is a float64 value)
+        return __fmul_rn(__fmul_rn(I, E.c), E.s[0]);
+    case SCMP_EPI_HEAD:    // sc/kernels.py:430-432
+        return __fmul_rn(I, __fmul_rn(E.c, E.s[batch]));
+    case SCMP_EPI_ZP_ROWCOL: {  // sc/kernels.py:1699-1707
+        const int64_t na = batch * E.sa_batch_stride + n;
+        const int64_t mb = batch * E.sb_batch_stride + m;
+        float raw = __fmul_rn(I, E.c);
+        const float za = E.za[na], zb = E.zb[mb];
+        const float t1 = __fmul_rn(-zb, E.suma[na]);
+        const float t2 = __fmul_rn(za, E.sumb[mb]);
+        const float t3 = __fmul_rn(__fmul_rn(E.dfloat, za), zb);
+        const float corr = __fadd_rn(__fsub_rn(t1, t2), t3);
+        raw = __fadd_rn(raw, corr);
+        return __fmul_rn(raw, __fmul_rn(E.sa[na], E.sb[mb]));
+    }
+    default: {  // SCMP_EPI_ZP_SCALAR, sc/kernels.py:1198-1204
+        float raw = __fmul_rn(I, E.c);
+        const float t1 = __fmul_rn(-E.zb[0], E.suma[batch * E.sa_batch_stride + n]);
+        const float t2 = __fmul_rn(E.za[0], E.sumb[batch * E.sb_batch_stride + m]);
+        const float corr = __fadd_rn(__fsub_rn(t1, t2), E.t3[0]);
+        raw = __fadd_rn(raw, corr);
+        return __fmul_rn(raw, E.s[0]);
+    }
+    }
+}
+
 int run_epilogue(const int32_t *iin, float *y, int64_t N, int64_t M, int64_t batch,
                  int64_t ldy, int64_t bsy, const scmp_epilogue &E, hipStream_t stream);
-int gemm_fp4_launch(const GemmP &P, int64_t batch, int JPF, int tile, bool chunked,
-                    hipStream_t stream);
+
+// FP4 kernel launchers, one translation unit per table width JPF (gemm_fp4_jp*.hip).
+// Non-chunked launches apply the epilogue in the kernel (y, or iout for SCMP_EPI_INT).
+template <int JPF>
+int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t stream);
+int gemm_fp4_launch(const GemmP &P, int64_t batch, int JPF, bool chunked, hipStream_t stream);
 
 }  // namespace scmp

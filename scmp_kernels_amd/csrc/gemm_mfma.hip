@@ -363,54 +363,15 @@ sc_gemm_mfma_kernel(GemmP P) {
     }
 }
 
-// fp32 epilogues of the reference paths, applied to the int32 accumulator in place.
+// fp32 epilogues of the reference paths, applied to the int32 accumulator in place
+// (int8 MFMA and VALU kernels; the FP4 kernel applies them itself).
 __global__ void epilogue_kernel(const int32_t *iin, float *y, int N, int M, int64_t ldy,
                                 int64_t bsy, scmp_epilogue E) {
     const int batch = blockIdx.z;
     for (int n = blockIdx.y; n < N; n += gridDim.y)
     for (int m = blockIdx.x * blockDim.x + threadIdx.x; m < M; m += gridDim.x * blockDim.x) {
         const int64_t o = batch * bsy + (int64_t)n * ldy + m;
-        const float I = (float)iin[o];
-        float out;
-        switch (E.kind) {
-        case SCMP_EPI_ROWCOL: {
-            // fl(fl(I*c) * fl(sa*sb)): sc/kernels.py:248 then :1707 / :1271 / :1894
-            float raw = __fmul_rn(I, E.c);
-            float s = __fmul_rn(E.sa[batch * E.sa_batch_stride + n],
-                                E.sb[batch * E.sb_batch_stride + m]);
-            out = __fmul_rn(raw, s);
-            break;
-        }
-        case SCMP_EPI_SCALAR:  // sc/kernels.py:1204 (scale product is a float64 value)
-            out = __fmul_rn(__fmul_rn(I, E.c), E.s[0]);
-            break;
-        case SCMP_EPI_HEAD:    // sc/kernels.py:430-432
-            out = __fmul_rn(I, __fmul_rn(E.c, E.s[batch]));
-            break;
-        case SCMP_EPI_ZP_ROWCOL: {  // sc/kernels.py:1699-1707
-            const int64_t na_ = batch * E.sa_batch_stride + n;
-            const int64_t mb_ = batch * E.sb_batch_stride + m;
-            float raw = __fmul_rn(I, E.c);
-            float za = E.za[na_], zb = E.zb[mb_];
-            float t1 = __fmul_rn(-zb, E.suma[na_]);
-            float t2 = __fmul_rn(za, E.sumb[mb_]);
-            float t3 = __fmul_rn(__fmul_rn(E.dfloat, za), zb);
-            float corr = __fadd_rn(__fsub_rn(t1, t2), t3);
-            raw = __fadd_rn(raw, corr);
-            out = __fmul_rn(raw, __fmul_rn(E.sa[na_], E.sb[mb_]));
-            break;
-        }
-        default: {  // SCMP_EPI_ZP_SCALAR, sc/kernels.py:1198-1204
-            float raw = __fmul_rn(I, E.c);
-            float t1 = __fmul_rn(-E.zb[0], E.suma[batch * E.sa_batch_stride + n]);
-            float t2 = __fmul_rn(E.za[0], E.sumb[batch * E.sb_batch_stride + m]);
-            float corr = __fadd_rn(__fsub_rn(t1, t2), E.t3[0]);
-            raw = __fadd_rn(raw, corr);
-            out = __fmul_rn(raw, E.s[0]);
-            break;
-        }
-        }
-        y[o] = out;
+        y[o] = epilogue_value(E, (float)iin[o], n, m, batch);
     }
 }
 
@@ -514,18 +475,19 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     P.chunk = chunked ? (int)a.chunk : 0;
     P.lut = a.lut; P.d_class = a.d_class; P.bipolar = a.bipolar;
     P.epi = a.epi; P.y = a.y; P.ldy = a.ldy; P.bsy = a.bsy;
-    // non-chunked: int32 I goes to iout, or into the fp32 output buffer itself (the
-    // epilogue pass then converts it in place)
-    P.iout = a.epi.kind == SCMP_EPI_INT ? a.iout : (int32_t *)a.y;
     P.tilesA = 0;
     P.nclass = a.nclass;
+    if (a.impl == SCMP_GEMM_MFMA_FP4) {
+        // the FP4 kernel applies the epilogue itself (int32 I for SCMP_EPI_INT)
+        P.iout = a.iout;
+        return gemm_fp4_launch(P, a.batch, a.JP < 32 ? 32 : a.JP, chunked, stream);
+    }
+    // int8 MFMA, non-chunked: int32 I goes to iout, or into the fp32 output buffer itself
+    // (the epilogue pass then converts it in place)
+    P.iout = a.epi.kind == SCMP_EPI_INT ? a.iout : (int32_t *)a.y;
     const bool perclass = a.d_class != nullptr;
-    int rc;
-    if (a.impl == SCMP_GEMM_MFMA_FP4)
-        rc = gemm_fp4_launch(P, a.batch, a.JP < 32 ? 32 : a.JP, a.tile, chunked, stream);
-    else
-        rc = perclass ? launch_pc<true>(P, a.batch, a.JP, a.tile, chunked, stream)
-                      : launch_pc<false>(P, a.batch, a.JP, a.tile, chunked, stream);
+    const int rc = perclass ? launch_pc<true>(P, a.batch, a.JP, a.tile, chunked, stream)
+                            : launch_pc<false>(P, a.batch, a.JP, a.tile, chunked, stream);
     if (rc != SCMP_OK || chunked || a.epi.kind == SCMP_EPI_INT) return rc;
     return run_epilogue(P.iout, a.y, a.N, a.M, a.batch, a.ldy, a.bsy, a.epi, stream);
 }

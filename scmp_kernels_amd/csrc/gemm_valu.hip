@@ -11,7 +11,7 @@
 // Each thread owns a 4 x 4 output micro-tile; a 256-thread workgroup covers 64 x 64.
 // Codes for 16 values of d at a time are staged through LDS; the bit-plane table of a
 // shared class lives in LDS for the whole kernel.
-#include "common.h"
+#include "gemm_common.h"
 
 namespace scmp {
 
@@ -90,38 +90,8 @@ sc_gemm_valu_kernel(const uint8_t *ca, int64_t lda, int64_t bsa, const uint8_t *
             if (m >= M) continue;
             const int64_t o = batch * bsy + (int64_t)n * ldy + m;
             const int I = acc[i][c];
-            float out;
-            switch (E.kind) {
-            case SCMP_EPI_INT: iout[o] = I; continue;
-            case SCMP_EPI_ROWCOL:
-                out = __fmul_rn(__fmul_rn((float)I, E.c),
-                                __fmul_rn(E.sa[batch * E.sa_batch_stride + n],
-                                          E.sb[batch * E.sb_batch_stride + m]));
-                break;
-            case SCMP_EPI_SCALAR: out = __fmul_rn(__fmul_rn((float)I, E.c), E.s[0]); break;
-            case SCMP_EPI_HEAD: out = __fmul_rn((float)I, __fmul_rn(E.c, E.s[batch])); break;
-            case SCMP_EPI_ZP_ROWCOL: {
-                const int64_t na_ = batch * E.sa_batch_stride + n;
-                const int64_t mb_ = batch * E.sb_batch_stride + m;
-                float raw = __fmul_rn((float)I, E.c);
-                float za = E.za[na_], zb = E.zb[mb_];
-                float t1 = __fmul_rn(-zb, E.suma[na_]);
-                float t2 = __fmul_rn(za, E.sumb[mb_]);
-                float t3 = __fmul_rn(__fmul_rn(E.dfloat, za), zb);
-                raw = __fadd_rn(raw, __fadd_rn(__fsub_rn(t1, t2), t3));
-                out = __fmul_rn(raw, __fmul_rn(E.sa[na_], E.sb[mb_]));
-                break;
-            }
-            default: {
-                float raw = __fmul_rn((float)I, E.c);
-                float t1 = __fmul_rn(-E.zb[0], E.suma[batch * E.sa_batch_stride + n]);
-                float t2 = __fmul_rn(E.za[0], E.sumb[batch * E.sb_batch_stride + m]);
-                raw = __fadd_rn(raw, __fadd_rn(__fsub_rn(t1, t2), E.t3[0]));
-                out = __fmul_rn(raw, E.s[0]);
-                break;
-            }
-            }
-            y[o] = out;
+            if (E.kind == SCMP_EPI_INT) iout[o] = I;
+            else y[o] = epilogue_value(E, (float)I, n, m, batch);
         }
     }
 }
