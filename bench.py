@@ -48,6 +48,43 @@ def make_cfg2(seed_a=1, seed_b=2, seed_ch=3):
     return a, b.astype(np.float32)
 
 
+def make_cfg3(seed_a=4, seed_b=5):
+    """ViT-B MLP: a = GELU(N(0,1)) (12608, 3072) = 64 images x 197 tokens, b ~ N(0, 0.02^2)
+    (768, 3072); GELU with erf, computed in float64 on the host then rounded to fp32."""
+    from math import sqrt
+    from scipy.special import erf
+    z = np.random.default_rng(seed_a).standard_normal((12608, 3072))
+    a = (0.5 * z * (1.0 + erf(z / sqrt(2.0)))).astype(np.float32)
+    b = (np.random.default_rng(seed_b).standard_normal((768, 3072)) * 0.02).astype(np.float32)
+    return a, b
+
+
+def make_cfg4(seed_q=6, seed_k=7, seed_p=8, seed_v=9, bh=768):
+    """ViT-B attention at batch 64 (BH = 768): q, k (BH, 197, 64) ~ N(0,1); P = row-softmax
+    of N(0,1) logits (BH, 197, 197); V^T (BH, 64, 197) ~ N(0,1)."""
+    q = np.random.default_rng(seed_q).standard_normal((bh, 197, 64), dtype=np.float32)
+    k = np.random.default_rng(seed_k).standard_normal((bh, 197, 64), dtype=np.float32)
+    z = np.random.default_rng(seed_p).standard_normal((bh, 197, 197))
+    z = np.exp(z - z.max(axis=-1, keepdims=True))
+    p = (z / z.sum(axis=-1, keepdims=True)).astype(np.float32)
+    vt = np.random.default_rng(seed_v).standard_normal((bh, 64, 197), dtype=np.float32)
+    return q, k, p, vt
+
+
+def make_cfg5(seed_a=10, seed_b=11, seed_rows=12):
+    """Mixed-precision unipolar: a (4096, 4096) ~ N(0,1) with 205 rows (5%, seeded choice)
+    replaced by Student-t (df = 3) rows; b (4096, 4096) ~ N(0, 0.02^2)."""
+    a = np.random.default_rng(seed_a).standard_normal((4096, 4096), dtype=np.float32)
+    rr = np.random.default_rng(seed_rows)
+    rows = rr.choice(4096, size=205, replace=False)
+    a[rows] = rr.standard_t(3, size=(205, 4096)).astype(np.float32)
+    b = (np.random.default_rng(seed_b).standard_normal((4096, 4096)) * 0.02).astype(np.float32)
+    return a, b
+
+
+CFG5_LEVELS = [256, 64, 16]
+
+
 def time_steps(fn, steps, warmup):
     import torch
     for _ in range(warmup):

@@ -1,58 +1,82 @@
-"""Unified public SC matmul entry point (the reference's scmp_kernels/sc/matmul.py:61-279).
+"""``sc_matmul``: the public SC matmul entry point, with the call surface of the
+reference's scmp_kernels/sc/matmul.py:61-279.
 
-``sc_matmul`` validates its arguments with the reference's messages, applies the
-halve_bipolar_stoc_len override, and dispatches by granularity / dimensionality /
-chunk_d to the host paths in :mod:`.kernels`. SmoothQuant's ``(a / s, b * s)``
-(matmul.py:189-190) is folded into the quantizer loads rather than materialized.
+The function checks its arguments (same ValueError messages as the reference), applies
+the ``halve_bipolar_stoc_len`` defaults, and hands the call to one host path of
+:mod:`.kernels` according to granularity, operand rank and ``chunk_d``. All work runs on
+the operands' GPU: the current device is switched to ``a.device`` for the call and
+restored afterwards. ``smooth_scales`` on fp32 operands is passed down to the quantizers,
+which divide / multiply as they load; other dtypes are smoothed up front.
 """
 from __future__ import annotations
 
 import contextlib
-import functools
 from typing import Optional
 
 import torch
 
-from .kernels import (
-    _sc_matmul_per_tensor,
-    _sc_matmul_per_row,
-    _sc_matmul_per_row_mlp,
-    _sc_matmul_per_row_batched,
-    _sc_matmul_per_head_bipolar,
-)
-from ..quant.smoothquant import apply_smoothing
+from . import kernels as _paths
+from ..quant.smoothquant import apply_smoothing, _check_smoothing_vector
 
 _VALID_GRANULARITIES = ("per_tensor", "per_row", "per_head")
 _VALID_MODES = ("bipolar", "unipolar")
 
 
-def _pin_to_operand_device(fn):
-    """Run on the operands' GPU; the previous current device is restored on exit
-    (scmp_kernels/sc/matmul.py:37-58)."""
-    @functools.wraps(fn)
-    def wrapper(a, b, *args, **kwargs):
-        if a.device != b.device:
-            raise ValueError(
-                f"sc_matmul: a and b must be on the same device, got a.device={a.device}, "
-                f"b.device={b.device}.")
-        if a.is_cuda:
-            with torch.cuda.device(a.device):
-                return fn(a, b, *args, **kwargs)
-        return fn(a, b, *args, **kwargs)
-    return wrapper
+def _device_scope(a: torch.Tensor, b: torch.Tensor):
+    """The context every launch of one call runs in: a's GPU as the current device (the
+    reference's device guard, scmp_kernels/sc/matmul.py:37-78). Operands on two devices
+    are rejected."""
+    if a.device != b.device:
+        raise ValueError(
+            f"sc_matmul: a and b must be on the same device, got a.device={a.device}, "
+            f"b.device={b.device}.")
+    return torch.cuda.device(a.device) if a.is_cuda else contextlib.nullcontext()
 
 
-@_pin_to_operand_device
+def _check_combination(a, b, granularity: str, mode: str, chunk_d: int) -> None:
+    """Reject unsupported argument combinations (scmp_kernels/sc/matmul.py:164-221)."""
+    if granularity not in _VALID_GRANULARITIES:
+        raise ValueError(f"sc_matmul: unknown granularity '{granularity}'. "
+                         f"Expected one of {_VALID_GRANULARITIES}.")
+    if mode not in _VALID_MODES:
+        raise ValueError(f"sc_matmul: unknown mode '{mode}'. Expected one of {_VALID_MODES}.")
+    ranks = f"a.dim()={a.dim()}, b.dim()={b.dim()}"
+    if chunk_d > 0:
+        why = None
+        if granularity != "per_row":
+            why = (f"requires granularity='per_row', got '{granularity}'. D-chunking is only "
+                   f"implemented in the per-row MLP fast path.")
+        elif mode != "bipolar":
+            why = (f"requires mode='bipolar', got '{mode}'. D-chunking is not implemented for "
+                   f"unipolar quantization.")
+        elif a.dim() != 2 or b.dim() != 2:
+            why = f"requires 2D inputs (the per-row MLP fast path is 2D only), got {ranks}."
+        if why:
+            raise ValueError(f"sc_matmul: chunk_d > 0 {why}")
+    if granularity == "per_head":
+        if a.dim() != 3 or b.dim() != 3:
+            raise ValueError(f"sc_matmul: granularity='per_head' requires 3D inputs "
+                             f"(BH, *, D), got {ranks}.")
+        if mode != "bipolar":
+            raise ValueError(f"sc_matmul: granularity='per_head' currently only supports "
+                             f"mode='bipolar', got '{mode}'.")
+
+
+def _smoothing_for_kernels(a, b, smooth_scales):
+    """(a, b, s): ``s`` for the quantizers to apply while loading fp32 operands, or
+    (a / s, b * s, None) for other dtypes."""
+    if smooth_scales is None:
+        return a, b, None
+    if a.dtype != torch.float32 or b.dtype != torch.float32:
+        a, b = apply_smoothing(a, b, smooth_scales)
+        return a, b, None
+    _check_smoothing_vector(smooth_scales, a.shape[-1], b.shape[-1], names=("a", "b"))
+    dev = a.device if a.is_cuda else torch.device("cuda")
+    return a, b, smooth_scales.to(device=dev, dtype=torch.float32).contiguous()
+
+
 @torch.no_grad()
-def sc_matmul(a: torch.Tensor, b: torch.Tensor, *args, **kwargs) -> torch.Tensor:
-    """Device-guarded public entry point; see :func:`_sc_matmul_impl`."""
-    guard = torch.cuda.device(a.device) if a.is_cuda else contextlib.nullcontext()
-    with guard:
-        return _sc_matmul_impl(a, b, *args, **kwargs)
-
-
-@torch.no_grad()
-def _sc_matmul_impl(
+def sc_matmul(
     a: torch.Tensor,
     b: torch.Tensor,
     granularity: str = "per_row",
@@ -68,96 +92,42 @@ def _sc_matmul_impl(
     halve_bipolar_stoc_len: bool = False,
     smooth_scales: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Stochastic-computing matmul ``a @ b.T`` (2-D ``(N, D) x (M, D) -> (N, M)`` or 3-D
-    ``(BH, N, D) x (BH, M, D) -> (BH, N, M)``), float32 output.
+    """Stochastic-computing ``a @ b.T``: ``(N, D) x (M, D) -> (N, M)`` or
+    ``(BH, N, D) x (BH, M, D) -> (BH, N, M)``, float32 (scmp_kernels/sc/matmul.py:61-163).
 
-    Arguments and errors are those of the reference (scmp_kernels/sc/matmul.py:82-163):
-    granularity in {"per_tensor", "per_row", "per_head"}, mode in {"bipolar",
-    "unipolar"}, stoc_len (default 2**sc_prec; at most 2**sc_prec), chunk_d (per_row
-    bipolar 2-D only), group_a / group_b row groups, rng_levels (default 2**sc_prec),
-    config (Sobol/LFSR RNG/SNG dict), halve_bipolar_stoc_len, smooth_scales (D,).
-    sc_prec must be in [1, 8] (8-bit operand codes).
+    granularity: "per_tensor" | "per_row" | "per_head"; mode: "bipolar" | "unipolar";
+    stoc_len: stream length (default 2**sc_prec, at most 2**sc_prec); chunk_d: per-row
+    bipolar 2-D inner-dimension chunks with their own scales; group_a / group_b: rows per
+    quantization group; rng_levels: RNG grid size (default 2**sc_prec); config: RNG/SNG
+    dict (default: one Sobol sequence per side); halve_bipolar_stoc_len: default
+    stoc_len and rng_levels to 2**(sc_prec-1) in bipolar mode; smooth_scales: (D,)
+    SmoothQuant vector, ``sc_matmul(a, b, smooth_scales=s) == sc_matmul(a / s, b * s)``.
+    sc_prec must lie in [1, 8] (byte operand codes).
     """
-    if granularity not in _VALID_GRANULARITIES:
-        raise ValueError(
-            f"sc_matmul: unknown granularity '{granularity}'. "
-            f"Expected one of {_VALID_GRANULARITIES}.")
-    if mode not in _VALID_MODES:
-        raise ValueError(
-            f"sc_matmul: unknown mode '{mode}'. "
-            f"Expected one of {_VALID_MODES}.")
-
-    if halve_bipolar_stoc_len and mode == "bipolar":
-        halved = 2 ** (sc_prec - 1)
-        if stoc_len is None:
-            stoc_len = halved
-        if rng_levels is None:
-            rng_levels = halved
-
-    smooth = None
-    if smooth_scales is not None:
-        if a.dtype == torch.float32 and b.dtype == torch.float32:
-            # validated here, applied inside the quantizers
-            if smooth_scales.dim() != 1:
-                raise ValueError(
-                    f"smooth_scales must be 1D (D,), got shape {tuple(smooth_scales.shape)}")
-            if a.shape[-1] != smooth_scales.shape[0] or b.shape[-1] != smooth_scales.shape[0]:
-                raise ValueError(
-                    f"D mismatch: a.shape[-1]={a.shape[-1]}, b.shape[-1]={b.shape[-1]}, "
-                    f"smooth_scales.shape[0]={smooth_scales.shape[0]}")
-            smooth = smooth_scales.to(device=a.device if a.is_cuda else "cuda",
-                                      dtype=torch.float32).contiguous()
-        else:
-            a, b = apply_smoothing(a, b, smooth_scales)
-
-    if chunk_d > 0:
-        if granularity != "per_row":
+    with _device_scope(a, b):
+        _check_combination(a, b, granularity, mode, chunk_d)
+        if halve_bipolar_stoc_len and mode == "bipolar":
+            half = 2 ** (sc_prec - 1)
+            stoc_len = half if stoc_len is None else stoc_len
+            rng_levels = half if rng_levels is None else rng_levels
+        if stoc_len is not None and stoc_len > 2 ** sc_prec:
             raise ValueError(
-                f"sc_matmul: chunk_d > 0 requires granularity='per_row', "
-                f"got '{granularity}'. D-chunking is only implemented in the "
-                f"per-row MLP fast path.")
-        if mode != "bipolar":
-            raise ValueError(
-                f"sc_matmul: chunk_d > 0 requires mode='bipolar', got '{mode}'. "
-                f"D-chunking is not implemented for unipolar quantization.")
-        if a.dim() != 2 or b.dim() != 2:
-            raise ValueError(
-                f"sc_matmul: chunk_d > 0 requires 2D inputs (the per-row MLP "
-                f"fast path is 2D only), got a.dim()={a.dim()}, b.dim()={b.dim()}.")
-
-    if granularity == "per_head":
-        if a.dim() != 3 or b.dim() != 3:
-            raise ValueError(
-                f"sc_matmul: granularity='per_head' requires 3D inputs (BH, *, D), "
-                f"got a.dim()={a.dim()}, b.dim()={b.dim()}.")
-        if mode != "bipolar":
-            raise ValueError(
-                f"sc_matmul: granularity='per_head' currently only supports "
-                f"mode='bipolar', got '{mode}'.")
-
-    if stoc_len is not None and stoc_len > 2 ** sc_prec:
-        raise ValueError(
-            f"sc_matmul: stoc_len={stoc_len} exceeds 2**sc_prec={2 ** sc_prec}; the RNG "
-            f"sequences are 2**sc_prec long.")
-
-    if granularity == "per_tensor":
-        return _sc_matmul_per_tensor(a, b, mode=mode, sc_prec=sc_prec, config=config,
-                                     stoc_len=stoc_len, rng_levels=rng_levels,
-                                     smooth_scales=smooth)
-    if granularity == "per_row":
+                f"sc_matmul: stoc_len={stoc_len} exceeds 2**sc_prec={2 ** sc_prec}; the RNG "
+                f"sequences are 2**sc_prec long.")
+        a, b, smooth = _smoothing_for_kernels(a, b, smooth_scales)
+        common = dict(mode=mode, sc_prec=sc_prec, config=config, stoc_len=stoc_len,
+                      rng_levels=rng_levels, smooth_scales=smooth)
+        if granularity == "per_tensor":
+            return _paths._sc_matmul_per_tensor(a, b, **common)
+        if granularity == "per_head":
+            del common["mode"]
+            return _paths._sc_matmul_per_head_bipolar(a, b, **common)
+        groups = dict(group_a=group_a, group_b=group_b)
         if chunk_d > 0:
-            return _sc_matmul_per_row_mlp(a, b, mode=mode, sc_prec=sc_prec, config=config,
-                                          group_a=group_a, group_b=group_b, chunk_d=chunk_d,
-                                          stoc_len=stoc_len, rng_levels=rng_levels,
-                                          smooth_scales=smooth)
+            return _paths._sc_matmul_per_row_mlp(a, b, chunk_d=chunk_d, **groups, **common)
         if a.dim() == 3:
-            return _sc_matmul_per_row_batched(a, b, group_a=group_a, group_b=group_b,
-                                              mode=mode, sc_prec=sc_prec, config=config,
-                                              stoc_len=stoc_len, rng_levels=rng_levels,
-                                              smooth_scales=smooth)
-        return _sc_matmul_per_row(a, b, group_a=group_a, group_b=group_b, mode=mode,
-                                  sc_prec=sc_prec, config=config, stoc_len=stoc_len,
-                                  rng_levels=rng_levels, smooth_scales=smooth)
-    return _sc_matmul_per_head_bipolar(a, b, sc_prec=sc_prec, config=config,
-                                       stoc_len=stoc_len, rng_levels=rng_levels,
-                                       smooth_scales=smooth)
+            return _paths._sc_matmul_per_row_batched(a, b, **groups, **common)
+        return _paths._sc_matmul_per_row(a, b, **groups, **common)
+
+
+_sc_matmul_impl = sc_matmul
