@@ -205,9 +205,20 @@ typedef struct scmp_gemm_args {
     int tile;                  /* MFMA tile preset (0 = default) */
     int nclass;                /* tables in lut; with d_class the FP4 kernel stages them in
                                   LDS when they fit (0: read them from global memory) */
+    void *workspace;           /* FP4 only: >= scmp_sc_gemm_workspace_bytes(args) bytes lets
+                                  the persistent kernel share tiles between workgroups so
+                                  that every CU gets equal work; NULL: whole tiles only */
+    int64_t workspace_bytes;
 } scmp_gemm_args;
 
 int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream);
+
+/* Workspace the FP4 kernel uses for args (0 when it would not share tiles): per-tile
+ * counters and two 256 x 256 slots of exact partial sums per persistent workgroup. The
+ * counters are reset by the library on the stream before each launch. No counterpart in
+ * the reference (its tiled kernel has one program per output tile,
+ * scmp_kernels/sc/kernels.py:838-866). */
+int64_t scmp_sc_gemm_workspace_bytes(const scmp_gemm_args *args);
 
 /* FP4 (e2m1) form of a stream table for SCMP_GEMM_MFMA_FP4: JPF = max(JP, 32) nibbles per
  * row (JPF / 2 bytes), dword u nibble b holds interval j' = (JPF/8)*b + u. Counts that e2m1

@@ -61,6 +61,7 @@ class GemmArgs(ctypes.Structure):
         ("bipolar", c_int), ("JP", c_int), ("lut", c_vp), ("d_class", c_vp), ("chunk", c_i64),
         ("epi", Epilogue), ("y", c_vp), ("iout", c_vp), ("ldy", c_i64), ("bsy", c_i64),
         ("impl", c_int), ("bitlut", c_vp), ("tile", c_int), ("nclass", c_int),
+        ("workspace", c_vp), ("workspace_bytes", c_i64),
     ]
 
 
@@ -68,7 +69,7 @@ EXPORTS = [
     "scmp_abi_version", "scmp_last_error", "scmp_rng_sobol", "scmp_rng_lfsr",
     "scmp_rng_expand", "scmp_rng_prepare", "scmp_build_stream_tables",
     "scmp_quant_workspace_bytes", "scmp_quantize", "scmp_sc_gemm", "scmp_build_bitlut",
-    "scmp_build_fp4_lut",
+    "scmp_build_fp4_lut", "scmp_sc_gemm_workspace_bytes",
 ]
 
 _lib = None
@@ -101,12 +102,15 @@ def load(path: str = LIB_PATH):
         lib.scmp_quant_workspace_bytes.restype = c_i64
         lib.scmp_quantize.argtypes = [ctypes.POINTER(QuantArgs), c_vp]
         lib.scmp_sc_gemm.argtypes = [ctypes.POINTER(GemmArgs), c_vp]
+        lib.scmp_sc_gemm_workspace_bytes.argtypes = [ctypes.POINTER(GemmArgs)]
+        lib.scmp_sc_gemm_workspace_bytes.restype = c_i64
         lib.scmp_build_bitlut.argtypes = [c_vp, c_int, c_int, c_vp, c_vp]
         lib.scmp_build_fp4_lut.argtypes = [c_vp, c_int, c_int, c_vp, c_vp, c_vp]
         for name in EXPORTS:
             getattr(lib, name).restype = getattr(lib, name).restype or c_int
         lib.scmp_last_error.restype = ctypes.c_char_p
         lib.scmp_quant_workspace_bytes.restype = c_i64
+        lib.scmp_sc_gemm_workspace_bytes.restype = c_i64
         _lib = lib
         return lib
 

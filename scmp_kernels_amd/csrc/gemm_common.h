@@ -26,8 +26,15 @@ struct GemmP {
     float *y;
     int32_t *iout;
     int64_t ldy, bsy;
-    int tilesA;
+    int tilesA, tilesB;
     int nclass;
+    // persistent FP4 schedule: ntiles = tilesA * tilesB * batch tiles of 256 x 256, nwg
+    // workgroups; split tiles keep exact partial sums in part (2 slots of 256 x 256 floats
+    // per workgroup) and count contributors in cnt (ntiles ints, zero on entry)
+    int64_t ntiles;
+    int nwg;
+    float *part;
+    int *cnt;
 };
 
 // fp32 epilogue of one output element (row n of A, row m of B, batch index) from its
@@ -77,6 +84,6 @@ int run_epilogue(const int32_t *iin, float *y, int64_t N, int64_t M, int64_t bat
 // Non-chunked launches apply the epilogue in the kernel (y, or iout for SCMP_EPI_INT).
 template <int JPF>
 int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t stream);
-int gemm_fp4_launch(const GemmP &P, int64_t batch, int JPF, bool chunked, hipStream_t stream);
+int gemm_fp4_run(GemmP &P, const scmp_gemm_args &a, bool chunked, hipStream_t stream);
 
 }  // namespace scmp

@@ -4,7 +4,63 @@
 
 namespace scmp {
 
-int gemm_fp4_launch(const GemmP &P, int64_t batch, int JPF, bool chunked, hipStream_t stream) {
+// Compute units of the current device (cached per device).
+static int device_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// Schedule of the non-chunked FP4 kernel (256 x 256 tiles, one workgroup per CU).
+struct Fp4Plan {
+    int64_t tilesA, tilesB, ntiles;
+    int nwg;                  // persistent workgroups
+    bool split;               // some tiles are shared by several workgroups
+    int64_t cnt_bytes, part_bytes;
+};
+
+// Each workgroup takes an equal share of the (tile, 8-d group) work list. Tiles are shared
+// only when it pays: inner dimension of at least 64 groups (512 d), and at least 32 groups
+// per workgroup. Otherwise every workgroup takes whole tiles.
+static Fp4Plan fp4_plan(int64_t N, int64_t M, int64_t D, int64_t batch, int ncu) {
+    Fp4Plan p;
+    p.tilesA = cdiv(N, 256);
+    p.tilesB = cdiv(M, 256);
+    p.ntiles = p.tilesA * p.tilesB * batch;
+    const int64_t G = cdiv(D, 8);
+    const int64_t W = p.ntiles * G;
+    int64_t nwg = p.ntiles;                      // whole tiles, one per workgroup
+    if (G >= 64) {
+        if (p.ntiles >= ncu) {
+            nwg = ncu;
+        } else {
+            nwg = W / 32;
+            if (nwg > ncu) nwg = ncu;
+            if (nwg < p.ntiles) nwg = p.ntiles;
+        }
+    }
+    p.nwg = (int)nwg;
+    p.split = (W % p.nwg) != 0 || (W / p.nwg) % G != 0;
+    p.cnt_bytes = (p.ntiles * 4 + 255) / 256 * 256;
+    p.part_bytes = (int64_t)p.nwg * 2 * 65536 * 4;
+    return p;
+}
+
+__global__ void zero_ints_kernel(int *p, int64_t n) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+static int fp4_launch_jpf(const GemmP &P, int64_t batch, int JPF, bool chunked,
+                          hipStream_t stream) {
     switch (JPF) {
     case 32: return gemm_fp4_launch_jpf<32>(P, batch, chunked, stream);
     case 64: return gemm_fp4_launch_jpf<64>(P, batch, chunked, stream);
@@ -12,6 +68,28 @@ int gemm_fp4_launch(const GemmP &P, int64_t batch, int JPF, bool chunked, hipStr
     case 256: return gemm_fp4_launch_jpf<256>(P, batch, chunked, stream);
     default: set_error("scmp_sc_gemm(fp4): JPF=%d unsupported", JPF); return SCMP_E_ARG;
     }
+}
+
+int gemm_fp4_run(GemmP &P, const scmp_gemm_args &a, bool chunked, hipStream_t stream) {
+    const int JPF = a.JP < 32 ? 32 : a.JP;
+    if (chunked) return fp4_launch_jpf(P, a.batch, JPF, true, stream);
+    Fp4Plan plan = fp4_plan(a.N, a.M, a.D, a.batch, device_cu_count());
+    P.tilesA = (int)plan.tilesA;
+    P.tilesB = (int)plan.tilesB;
+    P.ntiles = plan.ntiles;
+    P.part = nullptr;
+    P.cnt = nullptr;
+    P.nwg = (int)plan.ntiles;                 // whole tiles unless the workspace allows splits
+    if (plan.split && a.workspace && a.workspace_bytes >= plan.cnt_bytes + plan.part_bytes) {
+        P.nwg = plan.nwg;
+        P.cnt = (int *)a.workspace;
+        P.part = (float *)((uint8_t *)a.workspace + plan.cnt_bytes);
+        zero_ints_kernel<<<cdiv(plan.ntiles, 256), 256, 0, stream>>>(P.cnt, plan.ntiles);
+        SCMP_LAUNCH_CHECK("scmp_sc_gemm(fp4 counters)");
+    } else if (!plan.split) {
+        P.nwg = plan.nwg;                     // an even share of whole tiles each
+    }
+    return fp4_launch_jpf(P, a.batch, JPF, false, stream);
 }
 
 // FP4 table from the int8 stream table: row stride JPF/2 bytes, nibble layout above.
@@ -51,6 +129,14 @@ __global__ void fp4_lut_kernel(const int8_t *lut, int nclass, int JP, int JPF, u
 }  // namespace scmp
 
 using namespace scmp;
+
+extern "C" int64_t scmp_sc_gemm_workspace_bytes(const scmp_gemm_args *a) {
+    if (!a || a->impl != SCMP_GEMM_MFMA_FP4 || a->N <= 0 || a->M <= 0 || a->D <= 0 ||
+        a->batch <= 0 || (a->chunk > 0 && a->chunk < a->D))
+        return 0;
+    const Fp4Plan p = fp4_plan(a->N, a->M, a->D, a->batch, device_cu_count());
+    return p.split ? p.cnt_bytes + p.part_bytes : 0;
+}
 
 extern "C" int scmp_build_fp4_lut(const int8_t *lut, int nclass, int JP, uint8_t *lut4,
                                   int32_t *bad, hipStream_t stream) {

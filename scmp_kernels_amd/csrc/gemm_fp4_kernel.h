@@ -1,12 +1,13 @@
-// SC GEMM kernel on the gfx950 matrix cores with FP4 (e2m1) operands:
-// v_mfma_f32_32x32x64_f8f6f4 (cbsz = blgp = 4), twice the int8 rate on MI355X.
+// SC GEMM kernels on the gfx950 matrix cores with FP4 (e2m1) operands:
+// v_mfma_scale_f32_32x32x64_f8f6f4 (cbsz = blgp = 4, unit scales), twice the int8 rate.
 //
 // Same product as the int8 kernel (gemm_mfma.hip): I[n,m] = sum_d sum_{j' < JPF}
 // thermo(code_a)[j'] * lut[class(d)][code_b][j']. Every operand value is a small integer
 // that e2m1 represents exactly: the A side is 0 or +-1.0 (nibbles 0x0, 0x2, 0xA), the B
 // side an interval count 0..4 or 6 (0x0 0x2 0x4 0x5 0x6 0x7, sign bit 0x8). Products and
 // every partial sum are integers of magnitude <= 256 * D <= 2^24 (the host limits D to
-// 65536), so the fp32 accumulation is exact and (int)acc == I.
+// 65536), so the fp32 accumulation is exact and (int)acc == I; partial sums of disjoint
+// inner-dimension ranges add exactly in any order.
 //
 // One MFMA covers K = 64 intervals (lane half h: 32 nibbles = 4 dwords). Layout of one
 // JPF-nibble table row: dword u (JPF/8 of them), nibble b holds interval j' = (JPF/8)*b + u;
@@ -15,7 +16,19 @@
 // rows of tables in LDS selected by a code byte: the A thermometer table (row = THERMO
 // code) and the stream table (row = B code), so the inner loop is LDS reads and MFMAs.
 //
-// This header holds the kernel template; gemm_fp4_jp{32,64,128,256}.hip instantiate it
+// Two kernels:
+//  * sc_gemm_fp4_kernel — persistent and balanced. The work is the list of (tile, group of
+//    8 inner dimensions) pairs, tile-major; workgroup c takes the contiguous range
+//    [c*W/G, (c+1)*W/G) of W pairs, G = grid size, so every workgroup gets the same work
+//    whether or not the tile count divides the CU count. A tile whose groups are shared
+//    by several workgroups is finished by the last one to arrive: each contributor
+//    stores its exact partial sums to a workspace slot, then bumps the tile's counter;
+//    the one that sees the final count adds the others' slots and applies the epilogue.
+//    Nobody waits for anybody, so every workgroup runs to completion unconditionally.
+//  * sc_gemm_fp4_chunked_kernel — chunk_d: per-chunk fp32 epilogue summed in chunk
+//    order inside one workgroup (order-dependent, so never split across workgroups).
+//
+// This header holds the kernel templates; gemm_fp4_jp{32,64,128,256}.hip instantiate them
 // for one table width each (separate translation units compile in parallel).
 #pragma once
 
@@ -36,6 +49,9 @@ enum { LUT_LDS = 0, LUT_LDS_CLASSES = 1, LUT_GLOBAL = 2 };
 // floats of the per-wave epilogue staging area: one 32 x 32 block, rows padded to 33
 constexpr int kStageFloats = 32 * 33;
 
+// accelerator complex dies (XCDs) of an MI355X; workgroup i runs on XCD i mod 8
+constexpr int kXcds = 8;
+
 template <int JPF>
 struct Fp4Geom {
     static constexpr int ROWB = JPF / 2;                         // bytes per table row
@@ -52,12 +68,6 @@ struct Fp4Frag {
     v4i b[BB][Fp4Geom<JPF>::KS];
 };
 
-// The kernel reads both operands from tables indexed by a code byte:
-//   A: thermometer table T[code][j'] = sign(code) if j' < j(code) else 0 (built in LDS by
-//      the prologue, rows = THERMO code byte: bipolar sign bit | j, unipolar j);
-//   B: the stream table lut[class][code_b][j'].
-// Each k-step unit (one d, or two d for JPF = 32) is loaded one unit ahead into the other
-// of two fragment sets, so the LDS reads of unit u+1 overlap the MFMAs of unit u.
 // Interleave one unit's MFMAs with the next unit's LDS reads and address arithmetic:
 // per MFMA one DS read (while any remain) and NV VALU instructions.
 template <int NM, int NDS, int NV>
@@ -70,122 +80,75 @@ __device__ __forceinline__ void interleave_unit() {
     }
 }
 
-template <int JPF, int BA, int BB, int WA, int WB, int LUTSRC, bool CHUNKED, bool SCHED>
-__global__ void __launch_bounds__(64 * WA * WB)
-sc_gemm_fp4_kernel(GemmP P) {
+// LDS layout of both kernels: [thermometer table | stream table(s) | epilogue staging].
+template <int JPF, int LUTSRC>
+__device__ __forceinline__ int fp4_tables_bytes(const GemmP &P) {
     using G = Fp4Geom<JPF>;
-    constexpr int NT = 64 * WA * WB;
-    constexpr int ROWB = G::ROWB, KS = G::KS, UPG = G::UPG, LS = G::LS, TAB = G::TAB;
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    uint8_t *sA = smem;            // thermometer table
-    uint8_t *sB = smem + TAB;      // stream table(s) (LUT_LDS, LUT_LDS_CLASSES)
-    const uint8_t *glut = (const uint8_t *)P.lut;
+    return G::TAB * (1 + (LUTSRC == LUT_LDS ? 1 : LUTSRC == LUT_LDS_CLASSES ? P.nclass : 0));
+}
 
+// Prologue: the thermometer table T[code][j'] = sign(code) if j' < j(code) else 0 (rows =
+// THERMO code byte: bipolar sign bit | j, unipolar j), and the stream table(s) copied in.
+template <int JPF, int LUTSRC, int NT>
+__device__ __forceinline__ void fp4_load_tables(const GemmP &P, uint8_t *sA, uint8_t *sB) {
+    using G = Fp4Geom<JPF>;
+    constexpr int U = JPF / 8;                 // dwords per row
     const int tid = threadIdx.x;
-    {
-        constexpr int U = JPF / 8;                 // dwords per row
-        for (int e = tid; e < 256 * U; e += NT) {
-            const int row = e / U, u = e - row * U;
-            const int j = P.bipolar ? (row & 0x7f) : row;
-            const uint32_t one = (P.bipolar && (row & 0x80)) ? 0xAu : 0x2u;
-            uint32_t w = 0;
+    for (int e = tid; e < 256 * U; e += NT) {
+        const int row = e / U, u = e - row * U;
+        const int j = P.bipolar ? (row & 0x7f) : row;
+        const uint32_t one = (P.bipolar && (row & 0x80)) ? 0xAu : 0x2u;
+        uint32_t w = 0;
 #pragma unroll
-            for (int b = 0; b < 8; ++b)
-                if (U * b + u < j) w |= one << (4 * b);
-            *(uint32_t *)(sA + row * LS + 4 * u) = w;
-        }
-        if (LUTSRC != LUT_GLOBAL) {
-            constexpr int CH = ROWB / 16;         // 16-byte chunks per row
-            const int rows = (LUTSRC == LUT_LDS_CLASSES ? P.nclass : 1) * 256;
-            const v4i *src = (const v4i *)glut;
-            for (int e = tid; e < rows * CH; e += NT) {
-                const int row = e / CH, col = e - row * CH;
-                *(v4i *)(sB + row * LS + 16 * col) = src[e];
-            }
+        for (int b = 0; b < 8; ++b)
+            if (U * b + u < j) w |= one << (4 * b);
+        *(uint32_t *)(sA + row * G::LS + 4 * u) = w;
+    }
+    if (LUTSRC != LUT_GLOBAL) {
+        constexpr int CH = G::ROWB / 16;         // 16-byte chunks per row
+        const int rows = (LUTSRC == LUT_LDS_CLASSES ? P.nclass : 1) * 256;
+        const v4i *src = (const v4i *)P.lut;
+        for (int e = tid; e < rows * CH; e += NT) {
+            const int row = e / CH, col = e - row * CH;
+            *(v4i *)(sB + row * G::LS + 16 * col) = src[e];
         }
     }
-    __syncthreads();
+}
 
-    const int lane = tid & 63, wave = tid >> 6;
-    const int h = lane >> 5, li = lane & 31;
-    const int wa = wave % WA, wb = wave / WA;
-    const int ta = blockIdx.x % P.tilesA, tb = blockIdx.x / P.tilesA;
-    const int batch = blockIdx.z;
-    const int a0 = (ta * WA + wa) * (BA * 32);
-    const int b0 = (tb * WB + wb) * (BB * 32);
+// acc += the products of inner-dimension groups [g0, g1) (8 d per group) for the operand
+// rows at pa[i] (A, BA blocks of 32) and pb[c] (B, BB blocks of 32). Each k-step unit (one
+// d, or two d for JPF = 32) is loaded one unit ahead into the other of two fragment sets,
+// so the LDS reads of unit u+1 overlap the MFMAs of unit u; the code bytes of the next
+// group are fetched one group ahead. after(unit, dg) runs after each unit's MFMAs.
+template <int JPF, int BA, int BB, int LUTSRC, bool SCHED, class After>
+__device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA,
+                                               const uint8_t *sB, const uint8_t *const *pa,
+                                               const uint8_t *const *pb, int g0, int g1,
+                                               int h, v16f (&acc)[BA][BB], After after) {
+    using G = Fp4Geom<JPF>;
+    constexpr int ROWB = G::ROWB, KS = G::KS, UPG = G::UPG, LS = G::LS, TAB = G::TAB;
+    const uint8_t *glut = (const uint8_t *)P.lut;
     const int D = P.D;
-    const int ngroups = (D + 7) / 8;
-
-    const uint8_t *pa[BA];
-    const uint8_t *pb[BB];
-#pragma unroll
-    for (int i = 0; i < BA; ++i) pa[i] = P.ca + batch * P.bsa + (int64_t)(a0 + 32 * i + li) * P.lda;
-#pragma unroll
-    for (int c = 0; c < BB; ++c) pb[c] = P.cb + batch * P.bsb + (int64_t)(b0 + 32 * c + li) * P.ldb;
-
-    v16f acc[BA][BB];
-#pragma unroll
-    for (int i = 0; i < BA; ++i)
-#pragma unroll
-        for (int c = 0; c < BB; ++c) acc[i][c] = (v16f){0.0f};
-    float yac[CHUNKED ? BA : 1][CHUNKED ? BB : 1][16];
-    if (CHUNKED) {
-#pragma unroll
-        for (int i = 0; i < (CHUNKED ? BA : 1); ++i)
-#pragma unroll
-            for (int c = 0; c < (CHUNKED ? BB : 1); ++c)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) yac[i][c][r] = 0.0f;
-    }
-    const int chunk = P.chunk > 0 ? P.chunk : D;
-    int kchunk = 0;
-
-    // fp32 sum over inner-dimension chunks, in chunk order (sc/kernels.py:1333-1381)
-    auto flush_chunk = [&](int dlast) __attribute__((always_inline)) {
-        const bool end_chunk = ((dlast + 1) % chunk == 0) || (dlast + 1 >= D);
-        if (!(end_chunk && dlast < D)) return;
-        const float cc = P.epi.c;
-        const float *sa = P.epi.sa + (int64_t)kchunk * P.epi.sa_chunk_stride;
-        const float *sb = P.epi.sb + (int64_t)kchunk * P.epi.sb_chunk_stride;
-#pragma unroll
-        for (int c = 0; c < BB; ++c) {
-            const int m = b0 + 32 * c + li;
-            const float sbm = m < P.M ? sb[m] : 0.0f;
-#pragma unroll
-            for (int i = 0; i < BA; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                    const float san = n < P.N ? sa[n] : 0.0f;
-                    float raw = __fmul_rn(acc[i][c][r], cc);
-                    float term = __fmul_rn(raw, __fmul_rn(san, sbm));
-                    yac[CHUNKED ? i : 0][CHUNKED ? c : 0][r] =
-                        __fadd_rn(yac[CHUNKED ? i : 0][CHUNKED ? c : 0][r], term);
-                    acc[i][c][r] = 0.0f;
-                }
-        }
-        ++kchunk;
-    };
 
     // codes of the current group of 8 d (ca8 / cb8) and of the next one (na / nb)
     uint64_t ca8[BA], cb8[BB];
     uint2 na[BA], nb[BB];
 #pragma unroll
     for (int i = 0; i < BA; ++i) {
-        const uint2 v = *(const uint2 *)(pa[i]);
+        const uint2 v = *(const uint2 *)(pa[i] + 8 * g0);
         ca8[i] = ((uint64_t)v.y << 32) | v.x;
     }
 #pragma unroll
     for (int c = 0; c < BB; ++c) {
-        const uint2 v = *(const uint2 *)(pb[c]);
+        const uint2 v = *(const uint2 *)(pb[c] + 8 * g0);
         cb8[c] = ((uint64_t)v.y << 32) | v.x;
     }
     {
-        const int g1 = ngroups > 1 ? 1 : 0;
+        const int gn = g0 + 1 < g1 ? g0 + 1 : g1 - 1;
 #pragma unroll
-        for (int i = 0; i < BA; ++i) na[i] = *(const uint2 *)(pa[i] + 8 * g1);
+        for (int i = 0; i < BA; ++i) na[i] = *(const uint2 *)(pa[i] + 8 * gn);
 #pragma unroll
-        for (int c = 0; c < BB; ++c) nb[c] = *(const uint2 *)(pb[c] + 8 * g1);
+        for (int c = 0; c < BB; ++c) nb[c] = *(const uint2 *)(pb[c] + 8 * gn);
     }
 
     // load unit `unit` (of the group whose first d is dg) into F
@@ -222,16 +185,10 @@ sc_gemm_fp4_kernel(GemmP P) {
 #pragma unroll
                 for (int c = 0; c < BB; ++c) acc[i][c] = mfma_fp4(F.a[i][t], F.b[c][t], acc[i][c]);
     };
-    auto after = [&](int unit, int dg) __attribute__((always_inline)) {
-        if (CHUNKED) {
-            const int dlast = dg + (JPF == 32 ? 2 * unit + 1 : unit);
-            if (dg + (JPF == 32 ? 2 * unit : unit) < D) flush_chunk(dlast < D ? dlast : D - 1);
-        }
-    };
 
     Fp4Frag<JPF, BA, BB> F0, F1;
-    stage(F0, 0, 0);
-    for (int g = 0; g < ngroups; ++g) {
+    stage(F0, 0, 8 * g0);
+    for (int g = g0; g < g1; ++g) {
         const int dg = 8 * g;
 #pragma unroll
         for (int uu = 0; uu < UPG; uu += 2) {
@@ -243,12 +200,12 @@ sc_gemm_fp4_kernel(GemmP P) {
                 stage(F0, uu + 2, dg);
             } else {
                 // rotate to the next group; the group after it is fetched now (clamped to
-                // the last group, whose codes are then loaded but never used)
+                // the last group of the range, whose codes are then loaded but never used)
 #pragma unroll
                 for (int i = 0; i < BA; ++i) ca8[i] = ((uint64_t)na[i].y << 32) | na[i].x;
 #pragma unroll
                 for (int c = 0; c < BB; ++c) cb8[c] = ((uint64_t)nb[c].y << 32) | nb[c].x;
-                const int g2 = g + 2 < ngroups ? g + 2 : ngroups - 1;
+                const int g2 = g + 2 < g1 ? g + 2 : g1 - 1;
 #pragma unroll
                 for (int i = 0; i < BA; ++i) na[i] = *(const uint2 *)(pa[i] + 8 * g2);
 #pragma unroll
@@ -260,104 +217,316 @@ sc_gemm_fp4_kernel(GemmP P) {
             after(uu + 1, dg);
         }
     }
+}
 
-    if (CHUNKED) {
-        // the chunked fp32 sums are the final values
+// Balanced schedule: workgroup c of nwg owns work items [first(c), first(c+1)) of W.
+__device__ __forceinline__ int64_t sched_first(int64_t c, int64_t W, int64_t nwg) {
+    return c * W / nwg;
+}
+// The workgroup that owns work item u: the largest c with first(c) <= u.
+__device__ __forceinline__ int64_t sched_owner(int64_t u, int64_t W, int64_t nwg) {
+    return ((u + 1) * nwg - 1) / W;
+}
+// Partial-sum slot of workgroup c for tile t: 2c for its first segment, 2c + 1 for its
+// last one (a workgroup's range touches at most two shared tiles).
+__device__ __forceinline__ int64_t fp4_slot(int64_t c, int64_t t, int64_t W, int64_t nwg,
+                                            int ngroups) {
+    return 2 * c + (sched_first(c, W, nwg) / ngroups == t ? 0 : 1);
+}
+
+template <int JPF, int BA, int BB, int WA, int WB, int LUTSRC, bool SCHED>
+__global__ void __launch_bounds__(64 * WA * WB)
+sc_gemm_fp4_kernel(GemmP P) {
+    constexpr int NT = 64 * WA * WB;
+    constexpr int NW = WA * WB;
+    constexpr int TILE_FLOATS = NW * BA * BB * 1024;   // accumulators of one tile
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int s_last;
+    const int tabs = fp4_tables_bytes<JPF, LUTSRC>(P);
+    uint8_t *sA = smem;                                  // thermometer table
+    uint8_t *sB = smem + Fp4Geom<JPF>::TAB;              // stream table(s)
+    float *stg_all = (float *)(smem + ((tabs + 15) & ~15));
+
+    fp4_load_tables<JPF, LUTSRC, NT>(P, sA, sB);
+    __syncthreads();
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, li = lane & 31;
+    const int wa = wave % WA, wb = wave / WA;
+    const int ngroups = (P.D + 7) / 8;
+    const int64_t tiles_per_batch = (int64_t)P.tilesA * P.tilesB;
+    const int64_t W = P.ntiles * ngroups;
+    const int64_t nwg = gridDim.x;
+    // Workgroups are dispatched round-robin over the XCDs; number the workers so that
+    // consecutive ranges (the ones sharing a tile) run on the same XCD and its L2.
+    const int64_t c_self = nwg % kXcds == 0
+                               ? (blockIdx.x % kXcds) * (nwg / kXcds) + blockIdx.x / kXcds
+                               : (int64_t)blockIdx.x;
+    const int64_t u_end = sched_first(c_self + 1, W, nwg);
+    float *stg = stg_all + wave * kStageFloats;
+    const int ecol = lane & 31, ehalf = lane >> 5;
+
+    for (int64_t u = sched_first(c_self, W, nwg); u < u_end;) {
+        const int64_t t = u / ngroups;
+        const int g0 = (int)(u - t * ngroups);
+        const int g1 = (int)(u_end - t * ngroups < ngroups ? u_end - t * ngroups : ngroups);
+        const int64_t batch = t / tiles_per_batch;
+        const int64_t rem = t - batch * tiles_per_batch;
+        const int ta = (int)(rem % P.tilesA), tb = (int)(rem / P.tilesA);
+        const int a0 = (ta * WA + wa) * (BA * 32);
+        const int b0 = (tb * WB + wb) * (BB * 32);
+
+        const uint8_t *pa[BA];
+        const uint8_t *pb[BB];
 #pragma unroll
-        for (int c = 0; c < BB; ++c) {
-            const int m = b0 + 32 * c + li;
-            if (m >= P.M) continue;
+        for (int i = 0; i < BA; ++i)
+            pa[i] = P.ca + batch * P.bsa + (int64_t)(a0 + 32 * i + li) * P.lda;
+#pragma unroll
+        for (int c = 0; c < BB; ++c)
+            pb[c] = P.cb + batch * P.bsb + (int64_t)(b0 + 32 * c + li) * P.ldb;
+
+        v16f acc[BA][BB];
+#pragma unroll
+        for (int i = 0; i < BA; ++i)
+#pragma unroll
+            for (int c = 0; c < BB; ++c) acc[i][c] = (v16f){0.0f};
+        fp4_accumulate<JPF, BA, BB, LUTSRC, SCHED>(P, sA, sB, pa, pb, g0, g1, h, acc,
+                                                    [](int, int) {});
+
+        // Every accumulator block leaves its registers through this wave's LDS staging
+        // area only: it is written there, then read back row-wise (lanes 0-31 / 32-63
+        // take 32 consecutive m of rows 2k / 2k+1), and sink(i, c, rr, col, v) consumes
+        // the value of row rr, column col of block (i, c).
+        auto drain = [&](auto sink) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < BA; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (n >= P.N) continue;
-                    P.y[batch * P.bsy + (int64_t)n * P.ldy + m] =
-                        yac[CHUNKED ? i : 0][CHUNKED ? c : 0][r];
-                }
-        }
-        return;
-    }
-
-    // Fused epilogue. Each 32 x 32 accumulator block is staged through a per-wave LDS
-    // area (the tables are dead by now), then read back row-wise: lanes 0-31 / 32-63 take
-    // 32 consecutive m of rows 2k / 2k+1, so the fp32 stores are coalesced and the
-    // accumulator registers are only ever read by LDS stores.
-    __syncthreads();
-    float *stg = (float *)smem + wave * kStageFloats;
-    const int ecol = lane & 31, ehalf = lane >> 5;
+                for (int c = 0; c < BB; ++c) {
 #pragma unroll
-    for (int i = 0; i < BA; ++i)
-#pragma unroll
-        for (int c = 0; c < BB; ++c) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                stg[(8 * (r >> 2) + 4 * h + (r & 3)) * 33 + li] = acc[i][c][r];
-            __syncthreads();
-            const int m = b0 + 32 * c + ecol;
+                    for (int r = 0; r < 16; ++r)
+                        stg[(8 * (r >> 2) + 4 * h + (r & 3)) * 33 + li] = acc[i][c][r];
+                    __syncthreads();
 #pragma unroll 2
-            for (int rr = ehalf; rr < 32; rr += 2) {
-                const int n = a0 + 32 * i + rr;
-                const float v = stg[rr * 33 + ecol];
+                    for (int rr = ehalf; rr < 32; rr += 2) sink(i, c, rr, stg[rr * 33 + ecol]);
+                    __syncthreads();
+                }
+        };
+        // offset of (block, row, column) inside a partial-sum slot (row-major blocks)
+        auto pidx = [&](int i, int c, int rr) __attribute__((always_inline)) {
+            return (((wave * BA + i) * BB + c) * 32 + rr) * 32 + ecol;
+        };
+
+        const bool shared = g0 != 0 || g1 != ngroups;
+        bool finish = true;
+        int64_t cf = 0, cl = -1;
+        if (shared) {
+            // A tile shared with other workgroups: publish this workgroup's partial sums
+            // (slot 0: its first segment, slot 1: its last one), then count in; the
+            // workgroup that completes the count finishes the tile.
+            const int64_t tfirst = t * ngroups;
+            cf = sched_owner(tfirst, W, nwg);
+            cl = sched_owner(tfirst + ngroups - 1, W, nwg);
+            float *mine = P.part + fp4_slot(c_self, t, W, nwg, ngroups) * (int64_t)TILE_FLOATS;
+            drain([&](int i, int c, int rr, float v) __attribute__((always_inline)) {
+                mine[pidx(i, c, rr)] = v;
+            });
+            // The barrier waits for every wave's stores; one device-scope fence then
+            // publishes them (and, for the finisher, makes the others' visible: the L1
+            // and L2 invalidation it performs covers the whole CU).
+            __syncthreads();
+            if (tid == 0) {
+                __threadfence();
+                const int seen = atomicAdd(&P.cnt[t], 1);
+                const int last = seen == (int)(cl - cf);
+                if (last) {
+                    P.cnt[t] = 0;                    // ready for the next launch
+                    __threadfence();
+                }
+                s_last = last;
+            }
+            __syncthreads();
+            finish = s_last != 0;
+        }
+
+        if (finish) {
+            // fused epilogue, after adding the other contributors' exact partial sums
+            drain([&](int i, int c, int rr, float v) __attribute__((always_inline)) {
+                const int n = a0 + 32 * i + rr, m = b0 + 32 * c + ecol;
+                for (int64_t c2 = cf; c2 <= cl; ++c2) {
+                    if (c2 == c_self) continue;
+                    const float *other =
+                        P.part + fp4_slot(c2, t, W, nwg, ngroups) * (int64_t)TILE_FLOATS;
+                    v += __builtin_nontemporal_load(&other[pidx(i, c, rr)]);
+                }
                 if (n < P.N && m < P.M) {
                     const int64_t o = batch * P.bsy + (int64_t)n * P.ldy + m;
                     if (P.epi.kind == SCMP_EPI_INT) P.iout[o] = (int32_t)v;
                     else P.y[o] = epilogue_value(P.epi, v, n, m, batch);
                 }
-            }
-            __syncthreads();
+            });
         }
+        u = t * ngroups + g1;
+    }
+}
+
+template <int JPF, int BA, int BB, int WA, int WB, int LUTSRC>
+__global__ void __launch_bounds__(64 * WA * WB)
+sc_gemm_fp4_chunked_kernel(GemmP P) {
+    constexpr int NT = 64 * WA * WB;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint8_t *sA = smem;
+    uint8_t *sB = smem + Fp4Geom<JPF>::TAB;
+    fp4_load_tables<JPF, LUTSRC, NT>(P, sA, sB);
+    __syncthreads();
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, li = lane & 31;
+    const int wa = wave % WA, wb = wave / WA;
+    const int ta = blockIdx.x % P.tilesA, tb = blockIdx.x / P.tilesA;
+    const int batch = blockIdx.z;
+    const int a0 = (ta * WA + wa) * (BA * 32);
+    const int b0 = (tb * WB + wb) * (BB * 32);
+    const int D = P.D;
+    const int ngroups = (D + 7) / 8;
+
+    const uint8_t *pa[BA];
+    const uint8_t *pb[BB];
+#pragma unroll
+    for (int i = 0; i < BA; ++i) pa[i] = P.ca + batch * P.bsa + (int64_t)(a0 + 32 * i + li) * P.lda;
+#pragma unroll
+    for (int c = 0; c < BB; ++c) pb[c] = P.cb + batch * P.bsb + (int64_t)(b0 + 32 * c + li) * P.ldb;
+
+    v16f acc[BA][BB];
+    float yac[BA][BB][16];
+#pragma unroll
+    for (int i = 0; i < BA; ++i)
+#pragma unroll
+        for (int c = 0; c < BB; ++c) {
+            acc[i][c] = (v16f){0.0f};
+#pragma unroll
+            for (int r = 0; r < 16; ++r) yac[i][c][r] = 0.0f;
+        }
+    const int chunk = P.chunk;
+    int kchunk = 0;
+
+    // fp32 sum over inner-dimension chunks, in chunk order (sc/kernels.py:1333-1381):
+    // y += fl(fl(I_chunk * c) * fl(sa_chunk * sb_chunk)) after the chunk's last d
+    auto after = [&](int unit, int dg) __attribute__((always_inline)) {
+        const int dfirst = dg + (JPF == 32 ? 2 * unit : unit);
+        if (dfirst >= D) return;
+        const int dl = dg + (JPF == 32 ? 2 * unit + 1 : unit);
+        const int dlast = dl < D ? dl : D - 1;
+        if (!(((dlast + 1) % chunk == 0) || (dlast + 1 >= D))) return;
+        const float cc = P.epi.c;
+        const float *sa = P.epi.sa + (int64_t)kchunk * P.epi.sa_chunk_stride;
+        const float *sb = P.epi.sb + (int64_t)kchunk * P.epi.sb_chunk_stride;
+#pragma unroll
+        for (int c = 0; c < BB; ++c) {
+            const int m = b0 + 32 * c + li;
+            const float sbm = m < P.M ? sb[m] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < BA; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const float san = n < P.N ? sa[n] : 0.0f;
+                    const float raw = __fmul_rn(acc[i][c][r], cc);
+                    const float term = __fmul_rn(raw, __fmul_rn(san, sbm));
+                    yac[i][c][r] = __fadd_rn(yac[i][c][r], term);
+                    acc[i][c][r] = 0.0f;
+                }
+        }
+        ++kchunk;
+    };
+    fp4_accumulate<JPF, BA, BB, LUTSRC, false>(P, sA, sB, pa, pb, 0, ngroups, h, acc, after);
+
+#pragma unroll
+    for (int c = 0; c < BB; ++c) {
+        const int m = b0 + 32 * c + li;
+        if (m >= P.M) continue;
+#pragma unroll
+        for (int i = 0; i < BA; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (n >= P.N) continue;
+                P.y[batch * P.bsy + (int64_t)n * P.ldy + m] = yac[i][c][r];
+            }
+    }
 }
 
 // Largest LDS request of one workgroup (gfx950: 160 KiB per CU).
 constexpr int kFp4MaxLds = 160 * 1024;
 
-template <int JPF, int BA, int BB, int WA, int WB, int LUTSRC, bool CHUNKED, bool SCHED>
-static int launch_fp4_t(const GemmP &P0, int64_t batch, hipStream_t stream) {
-    using G = Fp4Geom<JPF>;
-    GemmP P = P0;
-    const int tileA = WA * BA * 32, tileB = WB * BB * 32;
-    P.tilesA = (int)cdiv(P.N, tileA);
-    const int64_t tilesB = cdiv(P.M, tileB);
-    const int ntab = LUTSRC == LUT_LDS ? 1 : LUTSRC == LUT_LDS_CLASSES ? P.nclass : 0;
-    size_t lds = (size_t)G::TAB * (1 + ntab);
-    const size_t stage = CHUNKED ? 0 : (size_t)WA * WB * kStageFloats * sizeof(float);
-    if (lds < stage) lds = stage;
-    auto kern = sc_gemm_fp4_kernel<JPF, BA, BB, WA, WB, LUTSRC, CHUNKED, SCHED>;
-    if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) {
-            set_error("scmp_sc_gemm(mfma fp4): %zu bytes of LDS refused: %s", lds,
-                      hipGetErrorString(e));
-            return SCMP_E_LAUNCH;
-        }
+template <class K>
+static int fp4_set_lds(K kern, size_t lds) {
+    if (lds <= 64 * 1024) return SCMP_OK;
+    hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) {
+        set_error("scmp_sc_gemm(mfma fp4): %zu bytes of LDS refused: %s", lds,
+                  hipGetErrorString(e));
+        return SCMP_E_LAUNCH;
     }
-    dim3 grid((unsigned)(P.tilesA * tilesB), 1, (unsigned)batch);
-    kern<<<grid, 64 * WA * WB, lds, stream>>>(P);
+    return SCMP_OK;
+}
+
+template <int JPF, int LUTSRC>
+static size_t fp4_tables_bytes_host(const GemmP &P) {
+    using G = Fp4Geom<JPF>;
+    return (size_t)G::TAB * (1 + (LUTSRC == LUT_LDS ? 1 : LUTSRC == LUT_LDS_CLASSES ? P.nclass : 0));
+}
+
+// Non-chunked: 256 x 256 tiles, each wave 128 x 128 (4 x 4 blocks of 32 x 32), MFMA /
+// LDS-read interleaving enforced, epilogue fused; P.nwg persistent workgroups (P.ntiles
+// when no split workspace was given: one tile each, no partial sums).
+template <int JPF, int LUTSRC>
+static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
+    constexpr int BA = 4, BB = 4, WA = 2, WB = 2;
+    GemmP P = P0;
+    auto kern = sc_gemm_fp4_kernel<JPF, BA, BB, WA, WB, LUTSRC, true>;
+    const size_t lds = ((fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15) +
+                       (size_t)WA * WB * kStageFloats * sizeof(float);
+    int rc = fp4_set_lds(kern, lds);
+    if (rc != SCMP_OK) return rc;
+    kern<<<dim3((unsigned)P.nwg), 64 * WA * WB, lds, stream>>>(P);
     SCMP_LAUNCH_CHECK("scmp_sc_gemm(mfma fp4)");
     return SCMP_OK;
 }
 
-// Tiles (A rows x B rows per workgroup):
-//  non-chunked: 256 x 256, each wave 128 x 128 (4 x 4 blocks of 32 x 32), MFMA / LDS-read
-//               interleaving enforced, epilogue fused;
-//  chunked:     128 x 128, each wave 64 x 64 (2 x 2 blocks, fp32 chunk sums in registers).
+// Chunked: 128 x 128 tiles, each wave 64 x 64 (2 x 2 blocks, fp32 chunk sums in registers).
 template <int JPF, int LUTSRC>
-static int launch_fp4_jp(const GemmP &P, int64_t batch, bool chunked, hipStream_t s) {
-    if (chunked) return launch_fp4_t<JPF, 2, 2, 2, 2, LUTSRC, true, false>(P, batch, s);
-    return launch_fp4_t<JPF, 4, 4, 2, 2, LUTSRC, false, true>(P, batch, s);
+static int launch_fp4_chunked(const GemmP &P0, int64_t batch, hipStream_t stream) {
+    constexpr int BA = 2, BB = 2, WA = 2, WB = 2;
+    GemmP P = P0;
+    P.tilesA = (int)cdiv(P.N, WA * BA * 32);
+    const int64_t tilesB = cdiv(P.M, WB * BB * 32);
+    auto kern = sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC>;
+    const size_t lds = fp4_tables_bytes_host<JPF, LUTSRC>(P);
+    int rc = fp4_set_lds(kern, lds);
+    if (rc != SCMP_OK) return rc;
+    kern<<<dim3((unsigned)(P.tilesA * tilesB), 1, (unsigned)batch), 64 * WA * WB, lds,
+           stream>>>(P);
+    SCMP_LAUNCH_CHECK("scmp_sc_gemm(mfma fp4, chunked)");
+    return SCMP_OK;
 }
 
-// Stream tables: one shared table in LDS; every class table in LDS when they fit;
-// otherwise per-class rows read from global memory.
+// Stream tables: one shared table in LDS; every class table in LDS when they fit
+// (leaving room for the epilogue staging); otherwise per-class rows from global memory.
 template <int JPF>
 int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t s) {
-    if (P.d_class == nullptr) return launch_fp4_jp<JPF, LUT_LDS>(P, batch, chunked, s);
-    if (P.nclass > 0 && (int64_t)Fp4Geom<JPF>::TAB * (1 + P.nclass) <= kFp4MaxLds)
-        return launch_fp4_jp<JPF, LUT_LDS_CLASSES>(P, batch, chunked, s);
-    return launch_fp4_jp<JPF, LUT_GLOBAL>(P, batch, chunked, s);
+    using G = Fp4Geom<JPF>;
+    const int64_t stage = 4 * kStageFloats * (int64_t)sizeof(float);
+    if (P.d_class == nullptr)
+        return chunked ? launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s)
+                       : launch_fp4_main<JPF, LUT_LDS>(P, batch, s);
+    if (P.nclass > 0 && (int64_t)G::TAB * (1 + P.nclass) + stage <= kFp4MaxLds)
+        return chunked ? launch_fp4_chunked<JPF, LUT_LDS_CLASSES>(P, batch, s)
+                       : launch_fp4_main<JPF, LUT_LDS_CLASSES>(P, batch, s);
+    return chunked ? launch_fp4_chunked<JPF, LUT_GLOBAL>(P, batch, s)
+                   : launch_fp4_main<JPF, LUT_GLOBAL>(P, batch, s);
 }
 
 }  // namespace scmp

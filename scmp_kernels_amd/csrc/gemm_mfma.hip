@@ -480,7 +480,7 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     if (a.impl == SCMP_GEMM_MFMA_FP4) {
         // the FP4 kernel applies the epilogue itself (int32 I for SCMP_EPI_INT)
         P.iout = a.iout;
-        return gemm_fp4_launch(P, a.batch, a.JP < 32 ? 32 : a.JP, chunked, stream);
+        return gemm_fp4_run(P, a, chunked, stream);
     }
     // int8 MFMA, non-chunked: int32 I goes to iout, or into the fp32 output buffer itself
     // (the epilogue pass then converts it in place)

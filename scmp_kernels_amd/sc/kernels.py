@@ -177,7 +177,14 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
     g.tile = int(os.environ.get("SCMP_GEMM_TILE", "0")) if tile is None else tile
     if g.impl == _lib.GEMM_VALU:
         g.bitlut = tabs.bitlut(stream).data_ptr()
-    _lib.check(_lib.load().scmp_sc_gemm(g, stream), "scmp_sc_gemm")
+    lib = _lib.load()
+    ws = None
+    nbytes = int(lib.scmp_sc_gemm_workspace_bytes(g))
+    if nbytes > 0:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        g.workspace, g.workspace_bytes = ws.data_ptr(), nbytes
+    _lib.check(lib.scmp_sc_gemm(g, stream), "scmp_sc_gemm")
+    return ws  # keep the workspace alive until the stream has consumed it
 
 
 def _codes(rows: int, D: int, device, batch: int = 0) -> torch.Tensor:

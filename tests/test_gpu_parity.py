@@ -250,6 +250,11 @@ GEMM_CASES = [
     (40, 31, 50, 16, 16, False),
     (65, 66, 129, 256, 256, False),
     (31, 129, 64, 32, 32, True),
+    # D >= 512: the FP4 kernel shares tiles between workgroups (split inner dimension,
+    # exact partial sums combined by the last contributor)
+    (300, 500, 1024, 256, 256, True),
+    (260, 270, 600, 128, 128, True),
+    (257, 300, 777, 64, 64, False),
 ]
 
 
