@@ -91,10 +91,10 @@ __global__ void reduce_kernel(scmp_quant_args a, int64_t group, int64_t segw, in
     }
 }
 
-__global__ void finalize_kernel(scmp_quant_args a, int64_t nunits, const uint32_t *stats,
-                                QParams *prm) {
-    int64_t u = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (u >= nunits) return;
+// Scale / reciprocal / zero-point of one (group, segment) from its reduced statistics
+// (stat0 = bits of max|x| or key(max), stat1 = key(-min)), in the operation order of the
+// variant's reference.
+__device__ QParams derive_params(const scmp_quant_args &a, uint32_t stat0, uint32_t stat1) {
     const float eps = 1e-5f;
     const float qf = (float)a.q_max;
     QParams p = {0.f, 0.f, 0.f, 0.f, 0.0, 0.0};
@@ -105,7 +105,7 @@ __global__ void finalize_kernel(scmp_quant_args a, int64_t nunits, const uint32_
         // max(|x|) clamped at 1e-5f; scale = A / Q; inv = 1 / scale (fused kernels,
         // quant/fused.py:76-79; per-head host math kernels.py:490-495; grouped
         // quant/grouped.py:46-47)
-        float A = fmax_first(__uint_as_float(stats[u * 2]), eps);
+        float A = fmax_first(__uint_as_float(stat0), eps);
         p.s = __fdiv_rn(A, qf);
         p.inv = __fdiv_rn(1.0f, p.s);
         p.s64 = (double)p.s;
@@ -114,7 +114,7 @@ __global__ void finalize_kernel(scmp_quant_args a, int64_t nunits, const uint32_
     case SCMP_Q_TENSOR_SYM: {
         // Python floats: max(|max|, |min|, 1e-5) / q_max; 1.0 / scale -> fp32 kernel arg
         // (sc/kernels.py:1173-1174, quant/fused.py:172-174)
-        double A = (double)__uint_as_float(stats[u * 2]);
+        double A = (double)__uint_as_float(stat0);
         A = A > 1e-5 ? A : 1e-5;
         p.s64 = __ddiv_rn(A, (double)a.q_max);
         p.inv = (float)__ddiv_rn(1.0, p.s64);
@@ -123,8 +123,8 @@ __global__ void finalize_kernel(scmp_quant_args a, int64_t nunits, const uint32_
     }
     case SCMP_Q_GROUP_ASYM: {
         // quant/grouped.py:111-115
-        float mx = float_of_key(stats[u * 2]);
-        float mn = -float_of_key(stats[u * 2 + 1]);
+        float mx = float_of_key(stat0);
+        float mn = -float_of_key(stat1);
         float range = fmax_first(__fsub_rn(mx, mn), eps);
         p.s = __fdiv_rn(range, qf);
         float z = rne(__fdiv_rn(-mn, p.s));
@@ -143,8 +143,8 @@ __global__ void finalize_kernel(scmp_quant_args a, int64_t nunits, const uint32_
         break;
     case SCMP_Q_TENSOR_ASYM: {
         // quant/fused.py:204-209 in Python floats
-        double mx = (double)float_of_key(stats[u * 2]);
-        double mn = -(double)float_of_key(stats[u * 2 + 1]);
+        double mx = (double)float_of_key(stat0);
+        double mn = -(double)float_of_key(stat1);
         double range = mx - mn;
         range = range > 1e-5 ? range : 1e-5;
         p.s64 = __ddiv_rn(range, (double)a.q_max);
@@ -157,7 +157,60 @@ __global__ void finalize_kernel(scmp_quant_args a, int64_t nunits, const uint32_
         break;
     }
     }
-    prm[u] = p;
+    return p;
+}
+
+__global__ void finalize_kernel(scmp_quant_args a, int64_t nunits, const uint32_t *stats,
+                                QParams *prm) {
+    int64_t u = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (u >= nunits) return;
+    prm[u] = derive_params(a, stats[u * 2], stats[u * 2 + 1]);
+}
+
+// The quantized integer of one element (pre-clamp value t, clamp to [qlo, Q]) in the
+// variant's operation order: division by the scale for the torch row-group quantizers,
+// multiplication by the reciprocal for the fused Triton ones.
+__device__ __forceinline__ float quant_value(const scmp_quant_args &a, const QParams &p,
+                                             float v, float qlo, float qf) {
+    float t;
+    switch (a.variant) {
+    case SCMP_Q_GROUP_SYM: t = __fdiv_rn(v, p.s); break;
+    case SCMP_Q_GROUP_ASYM: t = __fadd_rn(__fdiv_rn(v, p.s), p.zp); break;
+    case SCMP_Q_TENSOR_ASYM:
+    case SCMP_Q_HOST_ASYM: t = __fadd_rn(__fmul_rn(v, p.inv), p.zp); break;
+    default: t = __fmul_rn(v, p.inv); break;
+    }
+    return fmin_first(fmax_first(rne(t), qlo), qf);
+}
+
+// Writes the optional reference outputs of element (r, c) and returns its GEMM code byte.
+__device__ __forceinline__ uint8_t element_outputs(const scmp_quant_args &a, float q,
+                                                   int64_t r, int64_t c, bool asym, float rq,
+                                                   float rf, float qf) {
+    const int64_t o = r * a.out_ld + c;
+    if (a.beta16 || a.beta32) {
+        const float mag = fabsf(q);
+        const float bf = a.beta_formula == 0 ? __fmul_rn(mag, rq)
+                                             : __fdiv_rn(__fmul_rn(mag, rf), qf);
+        const int bv = (int)rne(bf);
+        if (a.beta16) a.beta16[o] = (int16_t)bv;
+        if (a.beta32) a.beta32[o] = bv;
+    }
+    if (a.sign) {
+        int8_t sg;
+        if (a.variant == SCMP_Q_GROUP_SYM) sg = q < 0.0f ? -1 : 1;
+        else sg = q > 0.0f ? 1 : (q < 0.0f ? -1 : 0);
+        a.sign[o] = sg;
+    }
+    if (a.xint) a.xint[o] = q;
+    if (!a.code) return 0;
+    const int qi = (int)q;
+    if (a.code_kind == SCMP_CODE_Q) return (uint8_t)(qi & 0xff);
+    const int cls = a.col_class ? a.col_class[c] : 0;
+    const int mi = qi < 0 ? -qi : qi;
+    uint8_t code = a.jtab[(int64_t)cls * 256 + mi];
+    if (!asym && qi < 0) code |= 0x80;
+    return code;
 }
 
 __global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, int64_t nseg,
@@ -190,45 +243,9 @@ __global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, 
         for (int64_t c = lane; c < a.cols; c += 64) {
             const int64_t sgi = c / segw;
             const QParams p = prm[g * nseg + sgi];
-            float v = load_x(a, r, c);
-            float t;
-            switch (a.variant) {
-            case SCMP_Q_GROUP_SYM: t = __fdiv_rn(v, p.s); break;
-            case SCMP_Q_GROUP_ASYM: t = __fadd_rn(__fdiv_rn(v, p.s), p.zp); break;
-            case SCMP_Q_TENSOR_ASYM:
-            case SCMP_Q_HOST_ASYM: t = __fadd_rn(__fmul_rn(v, p.inv), p.zp); break;
-            default: t = __fmul_rn(v, p.inv); break;
-            }
-            float q = fmin_first(fmax_first(rne(t), qlo), qf);
-            float mag = fabsf(q);
-            const int64_t o = r * a.out_ld + c;
-            if (a.beta16 || a.beta32) {
-                float bf = a.beta_formula == 0 ? __fmul_rn(mag, rq)
-                                               : __fdiv_rn(__fmul_rn(mag, rf), qf);
-                int bv = (int)rne(bf);
-                if (a.beta16) a.beta16[o] = (int16_t)bv;
-                if (a.beta32) a.beta32[o] = bv;
-            }
-            if (a.sign) {
-                int8_t sg;
-                if (a.variant == SCMP_Q_GROUP_SYM) sg = q < 0.0f ? -1 : 1;
-                else sg = q > 0.0f ? 1 : (q < 0.0f ? -1 : 0);
-                a.sign[o] = sg;
-            }
-            if (a.xint) a.xint[o] = q;
-            if (a.code) {
-                int qi = (int)q;
-                uint8_t code;
-                if (a.code_kind == SCMP_CODE_Q) {
-                    code = (uint8_t)(qi & 0xff);
-                } else {
-                    int cls = a.col_class ? a.col_class[c] : 0;
-                    int mi = qi < 0 ? -qi : qi;
-                    code = a.jtab[(int64_t)cls * 256 + mi];
-                    if (!asym && qi < 0) code |= 0x80;
-                }
-                a.code[crow * a.code_ld + c] = code;
-            }
+            const float q = quant_value(a, p, load_x(a, r, c), qlo, qf);
+            const uint8_t code = element_outputs(a, q, r, c, asym, rq, rf, qf);
+            if (a.code) a.code[crow * a.code_ld + c] = code;
             rsum += q;                            // exact: integers below 2^24
         }
         if (a.code)
@@ -248,6 +265,181 @@ __global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, 
     }
 }
 
+// ---------------------------------------------------------------------------------
+// One-pass quantizer for row groups (variants GROUP_SYM, GROUP_ASYM, ROW_SYM, HEAD_SYM
+// without column segments): one 256-thread workgroup per group of G rows reads the group
+// once, reduces its statistic, derives the scale and writes codes and outputs. Elements
+// go in chunks of 4 consecutive columns of a row; with REG the PT chunks of a thread stay
+// in registers between the passes, otherwise the second pass re-reads them (from L2).
+// The reduction performs the same max/min operations as reduce_kernel, so the statistic,
+// and everything derived from it, is bit-identical to the three-kernel pipeline.
+// ---------------------------------------------------------------------------------
+
+constexpr int kGroupThreads = 256;
+constexpr int kGroupMaxRows = 1024;       // row sums of a group live in LDS
+
+__device__ __forceinline__ void load_chunk(const scmp_quant_args &a, int64_t r, int64_t c,
+                                           bool vec, float (&v)[4]) {
+    const float *row = a.x + r * a.ld;
+    if (vec && c + 4 <= a.cols) {
+        const float4 x4 = *(const float4 *)(row + c);
+        v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;
+        if (a.smooth_mode != SCMP_SMOOTH_NONE) {
+            const float4 s4 = *(const float4 *)(a.smooth + c);
+            const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                v[k] = a.smooth_mode == SCMP_SMOOTH_DIV ? __fdiv_rn(v[k], sv[k])
+                                                        : __fmul_rn(v[k], sv[k]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = c + k < a.cols ? load_x(a, r, c + k) : 0.0f;
+}
+
+template <int PT, bool REG>
+__global__ void __launch_bounds__(kGroupThreads)
+quant_group_kernel(scmp_quant_args a, int64_t G, bool vec) {
+    __shared__ uint32_t red0[kGroupThreads / 64], red1[kGroupThreads / 64];
+    __shared__ float rsums[kGroupMaxRows];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * G;
+    const int64_t nr = a.rows - r0 < G ? a.rows - r0 : G;
+    const int64_t cpr = (a.cols + 3) / 4;            // chunks per row
+    const int64_t nch = nr * cpr;
+    const bool asym = is_asym(a.variant);
+    const bool want_sum = a.rowsum != nullptr;
+    if (want_sum)
+        for (int64_t i = tid; i < nr; i += kGroupThreads) rsums[i] = 0.0f;
+
+    // pass 1: statistic of the group
+    float vals[REG ? PT : 1][4];
+    float mx = -INFINITY, mn = INFINITY, am = 0.0f;
+    auto fold = [&](const float (&v)[4], int64_t c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (c + k >= a.cols) break;
+            if (asym) {
+                mx = fmaxf(mx, v[k]);
+                mn = fminf(mn, v[k]);
+            } else {
+                am = fmaxf(am, fabsf(v[k]));
+            }
+        }
+    };
+    if (REG) {
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            const int64_t ch = tid + (int64_t)k * kGroupThreads;
+            if (ch < nch) {
+                const int64_t rr = ch / cpr, c = 4 * (ch - rr * cpr);
+                load_chunk(a, r0 + rr, c, vec, vals[REG ? k : 0]);
+                fold(vals[REG ? k : 0], c);
+            }
+        }
+    } else {
+        for (int64_t ch = tid; ch < nch; ch += kGroupThreads) {
+            const int64_t rr = ch / cpr, c = 4 * (ch - rr * cpr);
+            float v[4];
+            load_chunk(a, r0 + rr, c, vec, v);
+            fold(v, c);
+        }
+    }
+    uint32_t k0, k1 = 0;
+    if (asym) {
+        mx = wave_max(mx);
+        mn = wave_min(mn);
+        k0 = key_of(mx);
+        k1 = key_of(-mn);
+    } else {
+        k0 = __float_as_uint(wave_max(am));
+    }
+    if (lane == 0) {
+        red0[wave] = k0;
+        red1[wave] = k1;
+    }
+    __syncthreads();
+    uint32_t s0 = red0[0], s1 = red1[0];
+#pragma unroll
+    for (int w = 1; w < kGroupThreads / 64; ++w) {
+        s0 = s0 > red0[w] ? s0 : red0[w];
+        s1 = s1 > red1[w] ? s1 : red1[w];
+    }
+    const QParams p = derive_params(a, s0, asym ? s1 : 0u);
+
+    // pass 2: codes and outputs
+    const float qf = (float)a.q_max;
+    const float qlo = asym ? 0.0f : (a.variant == SCMP_Q_HEAD_SYM ? -(qf + 1.0f) : -qf);
+    const float rq = __fdiv_rn((float)a.rng_levels, qf);
+    const float rf = (float)a.rng_levels;
+    const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+    auto emit = [&](const float (&v)[4], int64_t rr, int64_t c) __attribute__((always_inline)) {
+        const int64_t r = r0 + rr;
+        uint32_t word = 0;
+        float qs = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (c + k >= a.cols) break;
+            const float q = quant_value(a, p, v[k], qlo, qf);
+            word |= (uint32_t)element_outputs(a, q, r, c + k, asym, rq, rf, qf) << (8 * k);
+            qs += q;                                 // exact: integers below 2^24
+        }
+        if (a.code) {
+            const int64_t b = r / cbr, i = r - b * cbr;
+            *(uint32_t *)(a.code + (b * a.code_rows + i) * a.code_ld + c) = word;
+        }
+        if (want_sum) atomicAdd(&rsums[rr], qs);
+    };
+    if (REG) {
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            const int64_t ch = tid + (int64_t)k * kGroupThreads;
+            if (ch < nch) {
+                const int64_t rr = ch / cpr;
+                emit(vals[REG ? k : 0], rr, 4 * (ch - rr * cpr));
+            }
+        }
+    } else {
+        for (int64_t ch = tid; ch < nch; ch += kGroupThreads) {
+            const int64_t rr = ch / cpr, c = 4 * (ch - rr * cpr);
+            float v[4];
+            load_chunk(a, r0 + rr, c, vec, v);
+            emit(v, rr, c);
+        }
+    }
+    // zero code columns past the last 4-column chunk, per row of the group
+    if (a.code) {
+        const int64_t c0 = 4 * cpr;
+        const int64_t tail = a.code_ld - c0;
+        for (int64_t e = tid; e < nr * tail; e += kGroupThreads) {
+            const int64_t rr = e / tail, c = c0 + (e - rr * tail);
+            const int64_t r = r0 + rr, b = r / cbr, i = r - b * cbr;
+            a.code[(b * a.code_rows + i) * a.code_ld + c] = 0;
+        }
+    }
+    __syncthreads();
+    for (int64_t rr = tid; rr < nr; rr += kGroupThreads) {
+        const int64_t r = r0 + rr;
+        if (a.scale) a.scale[r] = p.s;
+        if (a.inv) a.inv[r] = p.inv;
+        if (a.zp) a.zp[r] = p.zp;
+        if (want_sum) a.rowsum[r] = rsums[rr];
+    }
+}
+
+// Zero the padding rows [code_batch_rows, code_rows) of every batch of a code buffer.
+__global__ void zero_code_rows_kernel(uint8_t *code, int64_t ld, int64_t code_rows,
+                                      int64_t cbr, int64_t nbatch) {
+    const int64_t per = (code_rows - cbr) * ld;
+    const int64_t total = per * nbatch;
+    for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t b = e / per, off = e - b * per;
+        code[(b * code_rows + cbr) * ld + off] = 0;
+    }
+}
+
 __global__ void tensor_out_kernel(const QParams *prm, double *scale64, double *zp64) {
     if (scale64) scale64[0] = prm[0].s64;
     if (zp64) zp64[0] = prm[0].zp64;
@@ -259,6 +451,36 @@ static inline void unit_counts(int64_t rows, int64_t cols, int64_t group, int64_
     *g = G;
     *segw = seg > 0 && seg < cols ? seg : (cols > 0 ? cols : 1);
     *nseg = cdiv(cols > 0 ? cols : 1, *segw);
+}
+
+// One workgroup per row group; PT (4-column chunks per thread) picks the register-held
+// variant when the group fits, otherwise the two-read variant.
+static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stream) {
+    const int64_t ngroups = cdiv(a.rows, G);
+    const int64_t chunks = G * cdiv(a.cols, 4);
+    const int64_t per = cdiv(chunks, kGroupThreads);
+    const bool vec = (a.ld % 4 == 0) && (((uintptr_t)a.x & 15) == 0) &&
+                     (a.smooth_mode == SCMP_SMOOTH_NONE || ((uintptr_t)a.smooth & 15) == 0);
+    const dim3 grid((unsigned)ngroups);
+    if (per <= 1) quant_group_kernel<1, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
+    else if (per <= 2) quant_group_kernel<2, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
+    else if (per <= 4) quant_group_kernel<4, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
+    else if (per <= 8) quant_group_kernel<8, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
+    else if (per <= 16) quant_group_kernel<16, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
+    else quant_group_kernel<1, false><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
+    SCMP_LAUNCH_CHECK("scmp_quantize/group");
+    if (a.code) {
+        const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+        if (a.code_rows > cbr) {
+            const int64_t total = (a.code_rows - cbr) * a.code_ld * (a.rows / cbr);
+            int64_t blocks = cdiv(total, 256);
+            if (blocks > 4096) blocks = 4096;
+            zero_code_rows_kernel<<<blocks, 256, 0, stream>>>(a.code, a.code_ld, a.code_rows,
+                                                              cbr, a.rows / cbr);
+            SCMP_LAUNCH_CHECK("scmp_quantize/pad");
+        }
+    }
+    return SCMP_OK;
 }
 
 }  // namespace scmp
@@ -315,6 +537,10 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
     QParams *prm = (QParams *)pa;
 
     const bool host = a.variant == SCMP_Q_HOST_SYM || a.variant == SCMP_Q_HOST_ASYM;
+    const bool tensor = a.variant == SCMP_Q_TENSOR_SYM || a.variant == SCMP_Q_TENSOR_ASYM;
+    if (!host && !tensor && nseg == 1 && G <= kGroupMaxRows && G * a.cols <= (1 << 22) &&
+        (!a.code || a.code_ld % 4 == 0))
+        return quantize_groups(a, G, stream);
     if (!host) {
         stats_init_kernel<<<cdiv(2 * nunits, 256), 256, 0, stream>>>(stats, 2 * nunits);
         SCMP_LAUNCH_CHECK("scmp_quantize/init");
