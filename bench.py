@@ -223,6 +223,59 @@ def bench_cfg2(args):
     }
 
 
+def bench_other(args):
+    """The other BASELINE configurations, timed as whole calls (inputs resident in HBM,
+    tables cached after the warmup); not the driver's headline metric."""
+    import torch
+    from scmp_kernels_amd import sc_matmul
+    from scmp_kernels_amd.mp import classify_rows_by_metric
+    dev = torch.device("cuda", 0)
+    T = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    if args.config == "cfg3":
+        a_h, b_h = make_cfg3()
+        a, b = T(a_h), T(b_h)
+        N, D = a.shape
+        M = b.shape[0]
+        B = N * M * D * 256
+        desc = "ViT-B MLP per_row bipolar chunk_d=72, 12608x768x3072"
+
+        def step():
+            return sc_matmul(a, b, "per_row", sc_prec=8, chunk_d=72)
+    elif args.config == "cfg4":
+        q_h, k_h, p_h, vt_h = make_cfg4()
+        q, k, p, vt = T(q_h), T(k_h), T(p_h), T(vt_h)
+        B = 2 * 768 * 197 * 197 * 64 * 256
+        desc = "attention per_head bipolar BH=768: QK^T (197x197x64) + P.V (197x64x197)"
+
+        def step():
+            sc_matmul(q, k, "per_head", sc_prec=8)
+            return sc_matmul(p, vt, "per_head", sc_prec=8)
+    elif args.config == "cfg5":
+        a_h, b_h = make_cfg5()
+        a, b = T(a_h), T(b_h)
+        metric = a.amax(dim=1) - a.amin(dim=1)
+        ra = classify_rows_by_metric(metric, CFG5_LEVELS, [1 / 3] * 3)
+        B = sum(len(ra.level_row_indices[L]) * 4096 * 4096 * L for L in CFG5_LEVELS)
+        desc = "mixed-level unipolar grouped (G=4), 4096x4096x4096, levels {256,64,16}"
+        Y = torch.empty((4096, 4096), dtype=torch.float32, device=dev)
+
+        def step():
+            for L in CFG5_LEVELS:
+                rows = ra.level_row_indices[L]
+                Y[rows] = sc_matmul(a[rows], b, "per_row", mode="unipolar", group_a=4,
+                                    group_b=4, stoc_len=L, rng_levels=L)
+            return Y
+    else:
+        raise SystemExit(f"unknown --config {args.config}")
+    t, _ = time_steps(step, args.steps, args.warmup)
+    log(f"{args.config}: {t * 1e3:.3f} ms per call")
+    return {"metric": f"ms & SC bit-ops/s per call ({desc})", "value": B / t,
+            "unit": "SC bit-ops/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(t * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "data": "synthetic (numpy PCG64, bench.py generators)",
+            "config": {"workload": args.config, "sc_bit_ops": B}}
+
+
 def profile_gemm(args):
     """One launch of the dominant kernel on the cfg2 operands, then one device copy of a
     known size (8 * 2^27 bytes each way) whose FETCH_SIZE / WRITE_SIZE counter values scale
@@ -308,6 +361,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.config in ("cfg3", "cfg4", "cfg5"):
+        print(json.dumps(bench_other(args)), flush=True)
+        return
     if args.config != "cfg2":
         print(f"unknown --config {args.config}", file=sys.stderr)
         sys.exit(2)
