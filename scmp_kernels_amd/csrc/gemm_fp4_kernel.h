@@ -56,7 +56,10 @@ template <int JPF>
 struct Fp4Geom {
     static constexpr int ROWB = JPF / 2;                         // bytes per table row
     static constexpr int KS = JPF >= 64 ? JPF / 64 : 1;          // MFMA k-steps per d
-    static constexpr int UPG = JPF == 32 ? 4 : 8;                // k-step units per 8 codes
+    // pipeline unit: KSU k-steps of one d (two d for JPF = 32); SPD units per d
+    static constexpr int KSU = KS > 2 ? 2 : KS;
+    static constexpr int SPD = KS / KSU;
+    static constexpr int UPG = JPF == 32 ? 4 : 8 * SPD;          // units per 8 codes
     // odd number of 16-byte chunks between LDS rows: spreads rows over the bank groups
     static constexpr int LS = 16 * ((ROWB / 16) | 1);
     static constexpr int TAB = 256 * LS;                          // one table in LDS
@@ -64,8 +67,8 @@ struct Fp4Geom {
 
 template <int JPF, int BA, int BB>
 struct Fp4Frag {
-    v4i a[BA][Fp4Geom<JPF>::KS];
-    v4i b[BB][Fp4Geom<JPF>::KS];
+    v4i a[BA][Fp4Geom<JPF>::KSU];
+    v4i b[BB][Fp4Geom<JPF>::KSU];
 };
 
 // Interleave one unit's MFMAs with the next unit's LDS reads and address arithmetic:
@@ -116,17 +119,19 @@ __device__ __forceinline__ void fp4_load_tables(const GemmP &P, uint8_t *sA, uin
 }
 
 // acc += the products of inner-dimension groups [g0, g1) (8 d per group) for the operand
-// rows at pa[i] (A, BA blocks of 32) and pb[c] (B, BB blocks of 32). Each k-step unit (one
-// d, or two d for JPF = 32) is loaded one unit ahead into the other of two fragment sets,
-// so the LDS reads of unit u+1 overlap the MFMAs of unit u; the code bytes of the next
-// group are fetched one group ahead. after(unit, dg) runs after each unit's MFMAs.
+// rows at pa[i] (A, BA blocks of 32) and pb[c] (B, BB blocks of 32). Each pipeline unit
+// (up to two k-steps of one d, or two d for JPF = 32) is loaded one unit ahead into the
+// other of two fragment sets, so the LDS reads of unit u+1 overlap the MFMAs of unit u;
+// the code bytes of the next group are fetched one group ahead. after(d0, d1) runs once
+// the MFMAs of inner dimensions d0..d1 are all issued.
 template <int JPF, int BA, int BB, int LUTSRC, bool SCHED, class After>
 __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA,
                                                const uint8_t *sB, const uint8_t *const *pa,
                                                const uint8_t *const *pb, int g0, int g1,
                                                int h, v16f (&acc)[BA][BB], After after) {
     using G = Fp4Geom<JPF>;
-    constexpr int ROWB = G::ROWB, KS = G::KS, UPG = G::UPG, LS = G::LS, TAB = G::TAB;
+    constexpr int ROWB = G::ROWB, KSU = G::KSU, SPD = G::SPD, UPG = G::UPG, LS = G::LS,
+                  TAB = G::TAB;
     const uint8_t *glut = (const uint8_t *)P.lut;
     const int D = P.D;
 
@@ -154,32 +159,38 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     // load unit `unit` (of the group whose first d is dg) into F
     auto stage = [&](Fp4Frag<JPF, BA, BB> &F, int unit, int dg)
         __attribute__((always_inline)) {
-        const int sh = JPF == 32 ? 8 * (2 * unit + h) : 8 * unit;
+        const int dl = JPF == 32 ? 2 * unit + h : unit / SPD;    // d within the group
+        const int sh = 8 * dl;
+        const int koff = (JPF == 32 ? 0 : 16 * h) + 32 * KSU * (unit % SPD);
 #pragma unroll
         for (int i = 0; i < BA; ++i) {
             const int code = (int)((ca8[i] >> sh) & 0xff);
-            const uint8_t *p = sA + code * LS + (JPF == 32 ? 0 : 16 * h);
+            const uint8_t *p = sA + code * LS + koff;
 #pragma unroll
-            for (int t = 0; t < KS; ++t) F.a[i][t] = *(const v4i *)(p + 32 * t);
+            for (int t = 0; t < KSU; ++t) F.a[i][t] = *(const v4i *)(p + 32 * t);
         }
         const uint8_t *base = sB;
         if (LUTSRC != LUT_LDS) {
-            const int d = dg + (JPF == 32 ? 2 * unit + h : unit);
+            const int d = dg + dl;
             const int cls = d < D ? P.d_class[d] : 0;
             base = LUTSRC == LUT_GLOBAL ? glut + (int64_t)cls * 256 * ROWB : sB + cls * TAB;
         }
 #pragma unroll
         for (int c = 0; c < BB; ++c) {
             const int code = (int)((cb8[c] >> sh) & 0xff);
-            const uint8_t *p = base + code * (LUTSRC == LUT_GLOBAL ? ROWB : LS) +
-                               (JPF == 32 ? 0 : 16 * h);
+            const uint8_t *p = base + code * (LUTSRC == LUT_GLOBAL ? ROWB : LS) + koff;
 #pragma unroll
-            for (int t = 0; t < KS; ++t) F.b[c][t] = *(const v4i *)(p + 32 * t);
+            for (int t = 0; t < KSU; ++t) F.b[c][t] = *(const v4i *)(p + 32 * t);
         }
+    };
+    auto done = [&](int unit, int dg) __attribute__((always_inline)) {
+        if (unit % SPD != SPD - 1) return;
+        if (JPF == 32) after(dg + 2 * unit, dg + 2 * unit + 1);
+        else after(dg + unit / SPD, dg + unit / SPD);
     };
     auto mma = [&](const Fp4Frag<JPF, BA, BB> &F) __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < KS; ++t)
+        for (int t = 0; t < KSU; ++t)
 #pragma unroll
             for (int i = 0; i < BA; ++i)
 #pragma unroll
@@ -194,8 +205,8 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         for (int uu = 0; uu < UPG; uu += 2) {
             stage(F1, uu + 1, dg);
             mma(F0);
-            if (SCHED) interleave_unit<BA * BB * KS, (BA + BB) * KS, 1>();
-            after(uu, dg);
+            if (SCHED) interleave_unit<BA * BB * KSU, (BA + BB) * KSU, 1>();
+            done(uu, dg);
             if (uu + 2 < UPG) {
                 stage(F0, uu + 2, dg);
             } else {
@@ -213,8 +224,8 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
                 stage(F0, 0, dg + 8);
             }
             mma(F1);
-            if (SCHED) interleave_unit<BA * BB * KS, (BA + BB) * KS, 1>();
-            after(uu + 1, dg);
+            if (SCHED) interleave_unit<BA * BB * KSU, (BA + BB) * KSU, 1>();
+            done(uu + 1, dg);
         }
     }
 }
@@ -413,10 +424,8 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
 
     // fp32 sum over inner-dimension chunks, in chunk order (sc/kernels.py:1333-1381):
     // y += fl(fl(I_chunk * c) * fl(sa_chunk * sb_chunk)) after the chunk's last d
-    auto after = [&](int unit, int dg) __attribute__((always_inline)) {
-        const int dfirst = dg + (JPF == 32 ? 2 * unit : unit);
+    auto after = [&](int dfirst, int dl) __attribute__((always_inline)) {
         if (dfirst >= D) return;
-        const int dl = dg + (JPF == 32 ? 2 * unit + 1 : unit);
         const int dlast = dl < D ? dl : D - 1;
         if (!(((dlast + 1) % chunk == 0) || (dlast + 1 >= D))) return;
         const float cc = P.epi.c;
