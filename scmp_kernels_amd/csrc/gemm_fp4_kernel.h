@@ -121,9 +121,12 @@ __device__ __forceinline__ void fp4_load_tables(const GemmP &P, uint8_t *sA, uin
 // acc += the products of inner-dimension groups [g0, g1) (8 d per group) for the operand
 // rows at pa[i] (A, BA blocks of 32) and pb[c] (B, BB blocks of 32). Each pipeline unit
 // (up to two k-steps of one d, or two d for JPF = 32) is loaded one unit ahead into the
-// other of two fragment sets, so the LDS reads of unit u+1 overlap the MFMAs of unit u;
-// the code bytes of the next group are fetched one group ahead. after(d0, d1) runs once
-// the MFMAs of inner dimensions d0..d1 are all issued.
+// other of two fragment sets, so the LDS reads of unit u+1 overlap the MFMAs of unit u.
+// The code bytes of a group (one uint2 per operand row) live in one of two buffers that
+// alternate by group parity: the loads for group g+2 are issued into the buffer group g
+// has just finished with, a whole group before they are read, and no register ever has
+// to wait for a load issued in the same group. after(d0, d1) runs once the MFMAs of
+// inner dimensions d0..d1 are all issued.
 template <int JPF, int BA, int BB, int LUTSRC, bool SCHED, class After>
 __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA,
                                                const uint8_t *sB, const uint8_t *const *pa,
@@ -132,40 +135,29 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     using G = Fp4Geom<JPF>;
     constexpr int ROWB = G::ROWB, KSU = G::KSU, SPD = G::SPD, UPG = G::UPG, LS = G::LS,
                   TAB = G::TAB;
+    constexpr int NR = BA + BB;                  // code rows per lane: A rows, then B rows
     const uint8_t *glut = (const uint8_t *)P.lut;
     const int D = P.D;
 
-    // codes of the current group of 8 d (ca8 / cb8) and of the next one (na / nb)
-    uint64_t ca8[BA], cb8[BB];
-    uint2 na[BA], nb[BB];
+    auto load_codes = [&](uint2 (&c)[NR], int g) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < BA; ++i) {
-        const uint2 v = *(const uint2 *)(pa[i] + 8 * g0);
-        ca8[i] = ((uint64_t)v.y << 32) | v.x;
-    }
+        for (int i = 0; i < BA; ++i) c[i] = *(const uint2 *)(pa[i] + 8 * g);
 #pragma unroll
-    for (int c = 0; c < BB; ++c) {
-        const uint2 v = *(const uint2 *)(pb[c] + 8 * g0);
-        cb8[c] = ((uint64_t)v.y << 32) | v.x;
-    }
-    {
-        const int gn = g0 + 1 < g1 ? g0 + 1 : g1 - 1;
-#pragma unroll
-        for (int i = 0; i < BA; ++i) na[i] = *(const uint2 *)(pa[i] + 8 * gn);
-#pragma unroll
-        for (int c = 0; c < BB; ++c) nb[c] = *(const uint2 *)(pb[c] + 8 * gn);
-    }
+        for (int j = 0; j < BB; ++j) c[BA + j] = *(const uint2 *)(pb[j] + 8 * g);
+    };
+    // code byte of inner dimension dl (0..7, a compile-time constant) of row r
+    auto code_of = [](const uint2 (&c)[NR], int r, int dl) __attribute__((always_inline)) {
+        return (int)(((dl < 4 ? c[r].x : c[r].y) >> (8 * (dl & 3))) & 0xffu);
+    };
 
-    // load unit `unit` (of the group whose first d is dg) into F
-    auto stage = [&](Fp4Frag<JPF, BA, BB> &F, int unit, int dg)
+    // load unit `unit` of the group whose first d is dg (codes in c) into F
+    auto stage = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&c)[NR], int unit, int dg)
         __attribute__((always_inline)) {
         const int dl = JPF == 32 ? 2 * unit + h : unit / SPD;    // d within the group
-        const int sh = 8 * dl;
         const int koff = (JPF == 32 ? 0 : 16 * h) + 32 * KSU * (unit % SPD);
 #pragma unroll
         for (int i = 0; i < BA; ++i) {
-            const int code = (int)((ca8[i] >> sh) & 0xff);
-            const uint8_t *p = sA + code * LS + koff;
+            const uint8_t *p = sA + code_of(c, i, dl) * LS + koff;
 #pragma unroll
             for (int t = 0; t < KSU; ++t) F.a[i][t] = *(const v4i *)(p + 32 * t);
         }
@@ -176,11 +168,11 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             base = LUTSRC == LUT_GLOBAL ? glut + (int64_t)cls * 256 * ROWB : sB + cls * TAB;
         }
 #pragma unroll
-        for (int c = 0; c < BB; ++c) {
-            const int code = (int)((cb8[c] >> sh) & 0xff);
-            const uint8_t *p = base + code * (LUTSRC == LUT_GLOBAL ? ROWB : LS) + koff;
+        for (int j = 0; j < BB; ++j) {
+            const uint8_t *p = base + code_of(c, BA + j, dl) * (LUTSRC == LUT_GLOBAL ? ROWB : LS) +
+                               koff;
 #pragma unroll
-            for (int t = 0; t < KSU; ++t) F.b[c][t] = *(const v4i *)(p + 32 * t);
+            for (int t = 0; t < KSU; ++t) F.b[j][t] = *(const v4i *)(p + 32 * t);
         }
     };
     auto done = [&](int unit, int dg) __attribute__((always_inline)) {
@@ -194,40 +186,52 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
 #pragma unroll
             for (int i = 0; i < BA; ++i)
 #pragma unroll
-                for (int c = 0; c < BB; ++c) acc[i][c] = mfma_fp4(F.a[i][t], F.b[c][t], acc[i][c]);
+                for (int j = 0; j < BB; ++j) acc[i][j] = mfma_fp4(F.a[i][t], F.b[j][t], acc[i][j]);
     };
 
     Fp4Frag<JPF, BA, BB> F0, F1;
-    stage(F0, 0, 8 * g0);
-    for (int g = g0; g < g1; ++g) {
+    // one group: its units from `cur`; the last unit stages unit 0 of the next group from
+    // `nxt` and refills `cur` with the group after that (clamped to the last group of the
+    // range, whose codes are then loaded but never used)
+    auto group = [&](uint2 (&cur)[NR], const uint2 (&nxt)[NR], int g)
+        __attribute__((always_inline)) {
         const int dg = 8 * g;
 #pragma unroll
         for (int uu = 0; uu < UPG; uu += 2) {
-            stage(F1, uu + 1, dg);
+            stage(F1, cur, uu + 1, dg);
             mma(F0);
-            if (SCHED) interleave_unit<BA * BB * KSU, (BA + BB) * KSU, 1>();
+            if (SCHED) {
+                interleave_unit<BA * BB * KSU, NR * KSU, 1>();
+                __builtin_amdgcn_sched_barrier(0);
+            }
             done(uu, dg);
             if (uu + 2 < UPG) {
-                stage(F0, uu + 2, dg);
+                stage(F0, cur, uu + 2, dg);
             } else {
-                // rotate to the next group; the group after it is fetched now (clamped to
-                // the last group of the range, whose codes are then loaded but never used)
-#pragma unroll
-                for (int i = 0; i < BA; ++i) ca8[i] = ((uint64_t)na[i].y << 32) | na[i].x;
-#pragma unroll
-                for (int c = 0; c < BB; ++c) cb8[c] = ((uint64_t)nb[c].y << 32) | nb[c].x;
-                const int g2 = g + 2 < g1 ? g + 2 : g1 - 1;
-#pragma unroll
-                for (int i = 0; i < BA; ++i) na[i] = *(const uint2 *)(pa[i] + 8 * g2);
-#pragma unroll
-                for (int c = 0; c < BB; ++c) nb[c] = *(const uint2 *)(pb[c] + 8 * g2);
-                stage(F0, 0, dg + 8);
+                load_codes(cur, g + 2 < g1 ? g + 2 : g1 - 1);
+                stage(F0, nxt, 0, dg + 8);
             }
             mma(F1);
-            if (SCHED) interleave_unit<BA * BB * KSU, (BA + BB) * KSU, 1>();
+            if (SCHED) {
+                interleave_unit<BA * BB * KSU, NR * KSU, 1>();
+                __builtin_amdgcn_sched_barrier(0);
+            }
             done(uu + 1, dg);
         }
+    };
+
+    uint2 cx0[NR], cx1[NR];
+    load_codes(cx0, g0);
+    load_codes(cx1, g0 + 1 < g1 ? g0 + 1 : g1 - 1);
+    stage(F0, cx0, 0, 8 * g0);
+    // pairs of groups, then an odd last group: the loop body has no branch, so the wait
+    // for a buffer's codes at the top of the loop only covers loads a group old
+    int g = g0;
+    for (; g + 1 < g1; g += 2) {
+        group(cx0, cx1, g);
+        group(cx1, cx0, g + 1);
     }
+    if (g < g1) group(cx0, cx1, g);
 }
 
 // Balanced schedule: workgroup c of nwg owns work items [first(c), first(c+1)) of W.
