@@ -269,57 +269,105 @@ __global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, 
 // One-pass quantizer for row groups (variants GROUP_SYM, GROUP_ASYM, ROW_SYM, HEAD_SYM
 // without column segments): one 256-thread workgroup per group of G rows reads the group
 // once, reduces its statistic, derives the scale and writes codes and outputs. Elements
-// go in chunks of 4 consecutive columns of a row; with REG the PT chunks of a thread stay
-// in registers between the passes, otherwise the second pass re-reads them (from L2).
+// go in chunks of 4 consecutive columns of a row; up to kMaxChunks chunks per thread stay
+// in registers between the passes, larger groups re-read their chunks (from L2).
 // The reduction performs the same max/min operations as reduce_kernel, so the statistic,
 // and everything derived from it, is bit-identical to the three-kernel pipeline.
+// The element operation (OP) and the smoothing mode (SM) are template parameters, so the
+// per-element path is straight-line code; chunk positions are tracked in 32-bit ints.
 // ---------------------------------------------------------------------------------
 
 constexpr int kGroupThreads = 256;
 constexpr int kGroupMaxRows = 1024;       // row sums of a group live in LDS
+constexpr int kMaxChunks = 16;            // register-held 4-column chunks per thread, max
 
-__device__ __forceinline__ void load_chunk(const scmp_quant_args &a, int64_t r, int64_t c,
-                                           bool vec, float (&v)[4]) {
+enum { QOP_DIV = 0, QOP_DIVZP = 1, QOP_MUL = 2 };
+
+// rne(fl(x / s)) (OP DIV) or rne(fl(fl(x / s) + zp)) (OP DIVZP), exactly, without the IEEE
+// division in the common case. y = fl(x * fl(1/s)) is within |x/s| * 1.2e-7 of x/s; for
+// |y| < 1024 that is < 1.3e-4, and the roundings of fl(x/s) and of the zero-point sum add
+// < 1.6e-4 more. So when y (or fl(y + zp)) lies farther than 2^-11 from every
+// half-integer, the exact value lies strictly on the same side of the same half-integer
+// and rounds to the same integer; otherwise (and for |y| >= 1024, inf, NaN) the exact
+// division decides.
+template <int OP>
+__device__ __forceinline__ float rne_quotient(float x, float s, float inv, float zp) {
+    const float y = __fmul_rn(x, inv);
+    if (__builtin_fabsf(y) < 1024.0f) {
+        const float u = OP == QOP_DIVZP ? __fadd_rn(y, zp) : y;
+        const float k = rne(u);
+        if (__builtin_fabsf(__fsub_rn(u, k)) < 0.5f - 4.8828125e-4f) return k;
+    }
+    const float t = __fdiv_rn(x, s);
+    return rne(OP == QOP_DIVZP ? __fadd_rn(t, zp) : t);
+}
+
+template <int SM>
+__device__ __forceinline__ void load_chunk4(const scmp_quant_args &a, int64_t r, int c,
+                                            bool vec, float (&v)[4]) {
     const float *row = a.x + r * a.ld;
     if (vec && c + 4 <= a.cols) {
         const float4 x4 = *(const float4 *)(row + c);
         v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;
-        if (a.smooth_mode != SCMP_SMOOTH_NONE) {
+        if (SM != SCMP_SMOOTH_NONE) {
             const float4 s4 = *(const float4 *)(a.smooth + c);
             const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                v[k] = a.smooth_mode == SCMP_SMOOTH_DIV ? __fdiv_rn(v[k], sv[k])
-                                                        : __fmul_rn(v[k], sv[k]);
+                v[k] = SM == SCMP_SMOOTH_DIV ? __fdiv_rn(v[k], sv[k]) : __fmul_rn(v[k], sv[k]);
         }
         return;
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = c + k < a.cols ? load_x(a, r, c + k) : 0.0f;
+    for (int k = 0; k < 4; ++k) {
+        float x = c + k < a.cols ? row[c + k] : 0.0f;
+        if (SM == SCMP_SMOOTH_DIV && c + k < a.cols) x = __fdiv_rn(x, a.smooth[c + k]);
+        if (SM == SCMP_SMOOTH_MUL && c + k < a.cols) x = __fmul_rn(x, a.smooth[c + k]);
+        v[k] = x;
+    }
 }
 
-template <int PT, bool REG>
+// PT: register-held chunks per thread (npt <= PT); npt > PT re-reads the chunks instead.
+template <int OP, int SM, int PT>
 __global__ void __launch_bounds__(kGroupThreads)
-quant_group_kernel(scmp_quant_args a, int64_t G, bool vec) {
+quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
     __shared__ uint32_t red0[kGroupThreads / 64], red1[kGroupThreads / 64];
     __shared__ float rsums[kGroupMaxRows];
+    __shared__ uint8_t s_jtab[256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t r0 = (int64_t)blockIdx.x * G;
-    const int64_t nr = a.rows - r0 < G ? a.rows - r0 : G;
-    const int64_t cpr = (a.cols + 3) / 4;            // chunks per row
-    const int64_t nch = nr * cpr;
-    const bool asym = is_asym(a.variant);
+    const int nr = a.rows - r0 < G ? (int)(a.rows - r0) : G;
+    const int nch = nr * cpr;                        // 4-column chunks of the group
+    constexpr bool asym = OP == QOP_DIVZP;
     const bool want_sum = a.rowsum != nullptr;
+    const bool thermo = a.code && a.code_kind == SCMP_CODE_THERMO;
+    const bool lds_jtab = thermo && a.col_class == nullptr;
     if (want_sum)
-        for (int64_t i = tid; i < nr; i += kGroupThreads) rsums[i] = 0.0f;
+        for (int i = tid; i < nr; i += kGroupThreads) rsums[i] = 0.0f;
+    if (lds_jtab) s_jtab[tid] = a.jtab[tid];
+
+    // position (row, first column) of this thread's k-th chunk, chunk index tid + 256 k
+    const int rr_first = tid / cpr;
+    const int cc_first = tid - rr_first * cpr;
+    auto advance = [&](int &rr, int &cc) __attribute__((always_inline)) {
+        cc += kGroupThreads;
+        while (cc >= cpr) {
+            cc -= cpr;
+            ++rr;
+        }
+    };
 
     // pass 1: statistic of the group
-    float vals[REG ? PT : 1][4];
+    const bool reg = npt <= PT;
+    float vals[PT][4];
     float mx = -INFINITY, mn = INFINITY, am = 0.0f;
-    auto fold = [&](const float (&v)[4], int64_t c) __attribute__((always_inline)) {
+    // Columns past the row end load as 0: harmless for max|x|, so only the asymmetric
+    // statistic of a row whose last chunk is partial checks the column bound.
+    const bool full = (a.cols & 3) == 0;
+    auto fold = [&](const float (&v)[4], int c) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            if (c + k >= a.cols) break;
+            if (asym && !full && c + k >= a.cols) break;
             if (asym) {
                 mx = fmaxf(mx, v[k]);
                 mn = fminf(mn, v[k]);
@@ -328,22 +376,23 @@ quant_group_kernel(scmp_quant_args a, int64_t G, bool vec) {
             }
         }
     };
-    if (REG) {
+    if (reg) {
+        int rr = rr_first, cc = cc_first;
 #pragma unroll
         for (int k = 0; k < PT; ++k) {
-            const int64_t ch = tid + (int64_t)k * kGroupThreads;
-            if (ch < nch) {
-                const int64_t rr = ch / cpr, c = 4 * (ch - rr * cpr);
-                load_chunk(a, r0 + rr, c, vec, vals[REG ? k : 0]);
-                fold(vals[REG ? k : 0], c);
+            if (k < npt && tid + k * kGroupThreads < nch) {
+                load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, vals[k]);
+                fold(vals[k], 4 * cc);
             }
+            advance(rr, cc);
         }
     } else {
-        for (int64_t ch = tid; ch < nch; ch += kGroupThreads) {
-            const int64_t rr = ch / cpr, c = 4 * (ch - rr * cpr);
+        int rr = rr_first, cc = cc_first;
+        for (int ch = tid; ch < nch; ch += kGroupThreads) {
             float v[4];
-            load_chunk(a, r0 + rr, c, vec, v);
-            fold(v, c);
+            load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, v);
+            fold(v, 4 * cc);
+            advance(rr, cc);
         }
     }
     uint32_t k0, k1 = 0;
@@ -374,14 +423,18 @@ quant_group_kernel(scmp_quant_args a, int64_t G, bool vec) {
     const float rq = __fdiv_rn((float)a.rng_levels, qf);
     const float rf = (float)a.rng_levels;
     const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
-    auto emit = [&](const float (&v)[4], int64_t rr, int64_t c) __attribute__((always_inline)) {
+    const bool api_out = a.beta16 || a.beta32 || a.sign || a.xint;
+    // General element path: any chunk, any requested outputs.
+    auto emit = [&](const float (&v)[4], int rr, int c) __attribute__((always_inline)) {
         const int64_t r = r0 + rr;
         uint32_t word = 0;
         float qs = 0.0f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             if (c + k >= a.cols) break;
-            const float q = quant_value(a, p, v[k], qlo, qf);
+            const float t = OP == QOP_MUL ? rne(__fmul_rn(v[k], p.inv))
+                                          : rne_quotient<OP>(v[k], p.s, p.inv, p.zp);
+            const float q = fmin_first(fmax_first(t, qlo), qf);
             word |= (uint32_t)element_outputs(a, q, r, c + k, asym, rq, rf, qf) << (8 * k);
             qs += q;                                 // exact: integers below 2^24
         }
@@ -391,35 +444,104 @@ quant_group_kernel(scmp_quant_args a, int64_t G, bool vec) {
         }
         if (want_sum) atomicAdd(&rsums[rr], qs);
     };
-    if (REG) {
+    // Hot path: full chunks, GEMM codes only (jtab in LDS). The four quotients take the
+    // multiply-by-reciprocal route together; one branch per chunk redoes all four with
+    // the exact division when any of them is within reach of a half-integer (see
+    // rne_quotient for the bound).
+    auto emit_fast = [&](const float (&v)[4], int rr, uint8_t *crow, int c)
+        __attribute__((always_inline)) {
+        float t[4];
+        if (OP == QOP_MUL) {
 #pragma unroll
-        for (int k = 0; k < PT; ++k) {
-            const int64_t ch = tid + (int64_t)k * kGroupThreads;
-            if (ch < nch) {
-                const int64_t rr = ch / cpr;
-                emit(vals[REG ? k : 0], rr, 4 * (ch - rr * cpr));
+            for (int k = 0; k < 4; ++k) t[k] = rne(__fmul_rn(v[k], p.inv));
+        } else {
+            bool ok = true;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float y = __fmul_rn(v[k], p.inv);
+                const float u = OP == QOP_DIVZP ? __fadd_rn(y, p.zp) : y;
+                t[k] = rne(u);
+                ok = ok && __builtin_fabsf(y) < 1024.0f &&
+                     __builtin_fabsf(__fsub_rn(u, t[k])) < 0.5f - 4.8828125e-4f;
+            }
+            if (!ok) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float e = __fdiv_rn(v[k], p.s);
+                    t[k] = rne(OP == QOP_DIVZP ? __fadd_rn(e, p.zp) : e);
+                }
             }
         }
+        uint32_t word = 0;
+        float qs = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float q = fmin_first(fmax_first(t[k], qlo), qf);
+            const int qi = (int)q;
+            uint32_t code;
+            if (thermo) {
+                code = s_jtab[qi < 0 ? -qi : qi];
+                if (!asym && qi < 0) code |= 0x80u;
+            } else {
+                code = (uint32_t)(qi & 0xff);
+            }
+            word |= code << (8 * k);
+            qs += q;
+        }
+        *(uint32_t *)(crow + c) = word;
+        if (want_sum) atomicAdd(&rsums[rr], qs);
+    };
+    const bool fast = full && !api_out && a.code && !(thermo && !lds_jtab);
+    if (reg && fast) {
+        // code row of input row r0 + rr: batch bb, row bi of the batch; tracked as rr grows
+        const int64_t rf0 = r0 + rr_first;
+        int64_t bb = rf0 / cbr, bi = rf0 - bb * cbr;
+        uint8_t *crow = a.code + (bb * a.code_rows + bi) * a.code_ld;
+        int rr = rr_first, cc = cc_first;
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            if (k < npt && tid + k * kGroupThreads < nch) emit_fast(vals[k], rr, crow, 4 * cc);
+            cc += kGroupThreads;
+            while (cc >= cpr) {
+                cc -= cpr;
+                ++rr;
+                if (++bi == cbr) {
+                    bi = 0;
+                    ++bb;
+                    crow = a.code + bb * a.code_rows * a.code_ld;
+                } else {
+                    crow += a.code_ld;
+                }
+            }
+        }
+    } else if (reg) {
+        int rr = rr_first, cc = cc_first;
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            if (k < npt && tid + k * kGroupThreads < nch) emit(vals[k], rr, 4 * cc);
+            advance(rr, cc);
+        }
     } else {
-        for (int64_t ch = tid; ch < nch; ch += kGroupThreads) {
-            const int64_t rr = ch / cpr, c = 4 * (ch - rr * cpr);
+        int rr = rr_first, cc = cc_first;
+        for (int ch = tid; ch < nch; ch += kGroupThreads) {
             float v[4];
-            load_chunk(a, r0 + rr, c, vec, v);
-            emit(v, rr, c);
+            load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, v);
+            emit(v, rr, 4 * cc);
+            advance(rr, cc);
         }
     }
     // zero code columns past the last 4-column chunk, per row of the group
     if (a.code) {
-        const int64_t c0 = 4 * cpr;
-        const int64_t tail = a.code_ld - c0;
-        for (int64_t e = tid; e < nr * tail; e += kGroupThreads) {
-            const int64_t rr = e / tail, c = c0 + (e - rr * tail);
+        const int c0 = 4 * cpr;
+        const int tail = (int)(a.code_ld - c0);
+        for (int e = tid; e < nr * tail; e += kGroupThreads) {
+            const int rr = e / tail, c = c0 + (e - rr * tail);
             const int64_t r = r0 + rr, b = r / cbr, i = r - b * cbr;
             a.code[(b * a.code_rows + i) * a.code_ld + c] = 0;
         }
     }
     __syncthreads();
-    for (int64_t rr = tid; rr < nr; rr += kGroupThreads) {
+    for (int rr = tid; rr < nr; rr += kGroupThreads) {
         const int64_t r = r0 + rr;
         if (a.scale) a.scale[r] = p.s;
         if (a.inv) a.inv[r] = p.inv;
@@ -453,21 +575,53 @@ static inline void unit_counts(int64_t rows, int64_t cols, int64_t group, int64_
     *nseg = cdiv(cols > 0 ? cols : 1, *segw);
 }
 
-// One workgroup per row group; PT (4-column chunks per thread) picks the register-held
-// variant when the group fits, otherwise the two-read variant.
+// One workgroup per row group, instantiated for the variant's element operation, the
+// smoothing mode and the register-held chunk count (4: rows up to 4096 columns; 16).
+template <int OP, int PT>
+static void launch_group_pt(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt,
+                            bool vec, hipStream_t stream) {
+    switch (a.smooth_mode) {
+    case SCMP_SMOOTH_DIV:
+        quant_group_kernel<OP, SCMP_SMOOTH_DIV, PT><<<grid, kGroupThreads, 0, stream>>>(
+            a, G, cpr, npt, vec);
+        break;
+    case SCMP_SMOOTH_MUL:
+        quant_group_kernel<OP, SCMP_SMOOTH_MUL, PT><<<grid, kGroupThreads, 0, stream>>>(
+            a, G, cpr, npt, vec);
+        break;
+    default:
+        quant_group_kernel<OP, SCMP_SMOOTH_NONE, PT><<<grid, kGroupThreads, 0, stream>>>(
+            a, G, cpr, npt, vec);
+        break;
+    }
+}
+
+template <int OP>
+static void launch_group(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt,
+                         bool vec, hipStream_t stream) {
+    if (npt <= 4) launch_group_pt<OP, 4>(a, grid, G, cpr, npt, vec, stream);
+    else launch_group_pt<OP, kMaxChunks>(a, grid, G, cpr, npt, vec, stream);
+}
+
 static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stream) {
     const int64_t ngroups = cdiv(a.rows, G);
-    const int64_t chunks = G * cdiv(a.cols, 4);
-    const int64_t per = cdiv(chunks, kGroupThreads);
+    const int64_t cpr = cdiv(a.cols, 4);
+    const int64_t per = cdiv(G * cpr, kGroupThreads);
     const bool vec = (a.ld % 4 == 0) && (((uintptr_t)a.x & 15) == 0) &&
                      (a.smooth_mode == SCMP_SMOOTH_NONE || ((uintptr_t)a.smooth & 15) == 0);
     const dim3 grid((unsigned)ngroups);
-    if (per <= 1) quant_group_kernel<1, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
-    else if (per <= 2) quant_group_kernel<2, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
-    else if (per <= 4) quant_group_kernel<4, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
-    else if (per <= 8) quant_group_kernel<8, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
-    else if (per <= 16) quant_group_kernel<16, true><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
-    else quant_group_kernel<1, false><<<grid, kGroupThreads, 0, stream>>>(a, G, vec);
+    const int npt = (int)(per <= kMaxChunks ? per : kMaxChunks + 1);
+    switch (a.variant) {
+    case SCMP_Q_GROUP_SYM:
+        launch_group<QOP_DIV>(a, grid, (int)G, (int)cpr, npt, vec, stream);
+        break;
+    case SCMP_Q_GROUP_ASYM:
+        launch_group<QOP_DIVZP>(a, grid, (int)G, (int)cpr, npt, vec, stream);
+        break;
+    default:
+        launch_group<QOP_MUL>(a, grid, (int)G, (int)cpr, npt, vec, stream);
+        break;
+    }
     SCMP_LAUNCH_CHECK("scmp_quantize/group");
     if (a.code) {
         const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
