@@ -189,6 +189,25 @@ def bench_cfg2(args):
         K.sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, iout=I, impl=impl)
 
     g_avg, g_min = gemm_event_time(gemm, max(3, args.steps))
+
+    # the two quantizer launches of a step, each timed alone: algorithmic HBM bytes =
+    # fp32 input read once + GEMM code bytes written (padded rows) + the smoothing vector
+    def quant_a():
+        K.quantize(a, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_DIV,
+                   code=ca, code_kind=_lib.CODE_THERMO, jtab=tabs.jtab)
+
+    def quant_b():
+        K.quantize(b, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_MUL,
+                   code=cb, code_kind=_lib.CODE_Q)
+
+    quants = {}
+    for name, fn, x, c in (("a", quant_a, a, ca), ("b", quant_b, b, cb)):
+        q_avg, _ = gemm_event_time(fn, max(5, args.steps))
+        nbytes = 4 * x.numel() + c.numel() + 4 * D
+        quants[name] = {"shape": list(x.shape), "avg_us": round(q_avg * 1e3, 2),
+                        "bytes": nbytes, "GB/s": round(nbytes / (q_avg * 1e-3) / 1e9, 1),
+                        "frac_of_8TB/s": round(nbytes / (q_avg * 1e-3) / 8e12, 3)}
+    log(f"quantizers: {quants}")
     log(f"SC GEMM kernel: avg {g_avg:.3f} ms, min {g_min:.3f} ms (JP={tabs.JP})")
     B = N * M * D * L
     ops, peak, unit, bound, kname = kernel_roofline(impl, N, M, D, tabs.JP)
@@ -219,6 +238,7 @@ def bench_cfg2(args):
                    "a": [N, D], "b": [M, D], "sc_prec": 8, "stoc_len": L,
                    "granularity": "per_row", "gemm_kernel": kname},
         "roofline": roof,
+        "quantizers": {"bound": "hbm", "peak_GB/s": 8000.0, **quants},
         "cpu_baseline": cpu,
     }
 

@@ -201,6 +201,63 @@ def test_quant_grouped_batched():
         _grouped_symmetric_quant_batched(T(x), 3, 127)
 
 
+def _near_half(seed, rows, cols, Q, asym):
+    """Rows whose quotients x / s sit at (or within 1e-4 of) half-integers, where the
+    quantizer's multiply-by-reciprocal shortcut must hand over to the exact division, plus
+    exact multiples of s and values at the clamp."""
+    rng = np.random.default_rng(seed)
+    A = (rng.uniform(0.5, 2.0, rows) * 10.0 ** rng.integers(-3, 3, rows)).astype(np.float32)
+    if asym:
+        lo = (-A * rng.uniform(0.0, 1.0, rows)).astype(np.float32)
+        s = (np.maximum(A - lo, np.float32(1e-5)) / np.float32(Q)).astype(np.float32)
+        zp = np.clip(np.rint((-lo / s).astype(np.float32)), 0, Q).astype(np.float32)
+        k = rng.integers(0, Q, (rows, cols)).astype(np.float32)
+        base = (-zp * s)[:, None]                # x / s + zp lands on k + frac + d
+    else:
+        s = (np.maximum(A, np.float32(1e-5)) / np.float32(Q)).astype(np.float32)
+        k = rng.integers(-Q, Q, (rows, cols)).astype(np.float32)
+        base = np.zeros((rows, 1), np.float32)
+    d = rng.choice(np.array([0.0, 1e-7, -1e-7, 3e-5, -3e-5, 1e-4, -1e-4, 0.25], np.float32),
+                   (rows, cols))
+    frac = np.where(rng.random((rows, cols)) < 0.8, np.float32(0.5), np.float32(0.0))
+    x = (base + (k + frac + d) * s[:, None]).astype(np.float32)
+    x = np.clip(x, (lo if asym else -A)[:, None], A[:, None]).astype(np.float32)
+    x[:, 0] = A                                  # pins the statistic of every row
+    if asym:
+        x[:, 1] = lo
+    return x
+
+
+@pytest.mark.parametrize("asym", [False, True])
+@pytest.mark.parametrize("smooth_mode", [0, 1, 2])
+def test_quant_codes_near_half_integers(asym, smooth_mode):
+    """GEMM code bytes of the row quantizers (codes-only path, full 4-column chunks) on
+    quotients placed at half-integers, against the oracle's exact-division quantizer."""
+    from scmp_kernels_amd import _lib
+    from scmp_kernels_amd.sc import kernels as K
+    rows, cols = 64, 256
+    Q = 255 if asym else 127
+    x = _near_half(7 + smooth_mode + 3 * asym, rows, cols, Q, asym)
+    sm = None
+    xs = x
+    if smooth_mode:
+        sm = np.random.default_rng(11).uniform(0.25, 4.0, cols).astype(np.float32)
+        xs = (x / sm if smooth_mode == 1 else x * sm).astype(np.float32)
+    if asym:
+        _, _, ref_q = O.grouped_asym(xs, 1, Q)
+    else:
+        _, ref_q, _ = O.grouped_sym(xs, 1, Q)
+    ref = (ref_q.astype(np.int32) & 0xff).astype(np.uint8)
+    code = torch.full((256, cols), 0x5A, dtype=torch.uint8, device=_dev())
+    ws = K.quantize(T(x), _lib.Q_GROUP_ASYM if asym else _lib.Q_GROUP_SYM, Q, 256,
+                    smooth=None if sm is None else T(sm), smooth_mode=smooth_mode,
+                    code=code, code_kind=_lib.CODE_Q)
+    got = code.cpu().numpy()
+    del ws
+    np.testing.assert_array_equal(got[:rows], ref)
+    assert not got[rows:].any()                  # padding rows are zero
+
+
 # -------------------------------------------------------------------------------------
 # the SC GEMM: integer accumulator against the oracle
 # -------------------------------------------------------------------------------------
