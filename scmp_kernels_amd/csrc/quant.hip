@@ -575,6 +575,176 @@ static inline void unit_counts(int64_t rows, int64_t cols, int64_t group, int64_
     *nseg = cdiv(cols > 0 ? cols : 1, *segw);
 }
 
+// ---------------------------------------------------------------------------------
+// One-pass quantizer for one-row groups split into column segments (chunk_d): one
+// 256-thread workgroup per row keeps the row in registers; every 4-column chunk lies in
+// one segment (segment width a multiple of 4), folds its statistic into the segment's
+// LDS slot with the same order-independent atomic max as reduce_kernel, and the segment
+// parameters are derived once per segment in LDS.
+// ---------------------------------------------------------------------------------
+
+constexpr int kMaxSegs = 256;
+
+template <int OP, int SM, int PT>
+__global__ void __launch_bounds__(kGroupThreads)
+quant_seg_kernel(scmp_quant_args a, int cpr, int segw, int nseg, bool vec) {
+    __shared__ uint32_t s_st0[kMaxSegs], s_st1[kMaxSegs];
+    __shared__ QParams s_prm[kMaxSegs];
+    __shared__ uint8_t s_jtab[256];
+    __shared__ float s_rsum;
+    const int tid = threadIdx.x;
+    const int64_t r = blockIdx.x;
+    constexpr bool asym = OP == QOP_DIVZP;
+    const bool thermo = a.code && a.code_kind == SCMP_CODE_THERMO;
+    const bool lds_jtab = thermo && a.col_class == nullptr;
+    for (int t = tid; t < nseg; t += kGroupThreads) s_st0[t] = s_st1[t] = 0u;
+    if (lds_jtab) s_jtab[tid] = a.jtab[tid];
+    if (tid == 0) s_rsum = 0.0f;
+    __syncthreads();
+
+    float vals[PT][4];
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+        const int cc = tid + k * kGroupThreads;
+        if (cc < cpr) {
+            const int c = 4 * cc;
+            load_chunk4<SM>(a, r, c, vec, vals[k]);
+            float mx = -INFINITY, mn = INFINITY, am = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (c + e >= a.cols) break;
+                if (asym) {
+                    mx = fmaxf(mx, vals[k][e]);
+                    mn = fminf(mn, vals[k][e]);
+                } else {
+                    am = fmaxf(am, fabsf(vals[k][e]));
+                }
+            }
+            const int sg = (unsigned)c / (unsigned)segw;
+            if (asym) {
+                atomicMax(&s_st0[sg], key_of(mx));
+                atomicMax(&s_st1[sg], key_of(-mn));
+            } else {
+                atomicMax(&s_st0[sg], __float_as_uint(am));
+            }
+        }
+    }
+    __syncthreads();
+    for (int t = tid; t < nseg; t += kGroupThreads)
+        s_prm[t] = derive_params(a, s_st0[t], asym ? s_st1[t] : 0u);
+    __syncthreads();
+
+    const float qf = (float)a.q_max;
+    const float qlo = asym ? 0.0f : (a.variant == SCMP_Q_HEAD_SYM ? -(qf + 1.0f) : -qf);
+    const float rq = __fdiv_rn((float)a.rng_levels, qf);
+    const float rf = (float)a.rng_levels;
+    const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+    const int64_t bb = r / cbr, bi = r - bb * cbr;
+    uint8_t *crow = a.code ? a.code + (bb * a.code_rows + bi) * a.code_ld : nullptr;
+    const bool api_out = a.beta16 || a.beta32 || a.sign || a.xint;
+    const bool fast = !api_out && a.code && !(thermo && !lds_jtab);
+    float qs = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+        const int cc = tid + k * kGroupThreads;
+        if (cc < cpr) {
+            const int c = 4 * cc;
+            const QParams &p = s_prm[(unsigned)c / (unsigned)segw];
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (c + e >= a.cols) break;
+                const float t = OP == QOP_MUL ? rne(__fmul_rn(vals[k][e], p.inv))
+                                              : rne_quotient<OP>(vals[k][e], p.s, p.inv, p.zp);
+                const float q = fmin_first(fmax_first(t, qlo), qf);
+                uint32_t code;
+                if (fast) {
+                    const int qi = (int)q;
+                    if (thermo) {
+                        code = s_jtab[qi < 0 ? -qi : qi];
+                        if (!asym && qi < 0) code |= 0x80u;
+                    } else {
+                        code = (uint32_t)(qi & 0xff);
+                    }
+                } else {
+                    code = element_outputs(a, q, r, c + e, asym, rq, rf, qf);
+                }
+                word |= code << (8 * e);
+                qs += q;                             // exact: integers below 2^24
+            }
+            if (crow) *(uint32_t *)(crow + c) = word;
+        }
+    }
+    if (crow)
+        for (int64_t c = 4 * (int64_t)cpr + tid; c < a.code_ld; c += kGroupThreads) crow[c] = 0;
+    if (a.rowsum) atomicAdd(&s_rsum, qs);
+    __syncthreads();
+    for (int t = tid; t < nseg; t += kGroupThreads) {
+        if (a.scale) a.scale[(int64_t)t * a.rows + r] = s_prm[t].s;
+        if (a.inv) a.inv[(int64_t)t * a.rows + r] = s_prm[t].inv;
+    }
+    if (tid == 0) {
+        if (a.zp) a.zp[r] = s_prm[0].zp;
+        if (a.rowsum) a.rowsum[r] = s_rsum;
+    }
+}
+
+template <int OP, int PT>
+static void launch_seg_pt(const scmp_quant_args &a, int cpr, int segw, int nseg, bool vec,
+                          hipStream_t stream) {
+    const dim3 grid((unsigned)a.rows);
+    switch (a.smooth_mode) {
+    case SCMP_SMOOTH_DIV:
+        quant_seg_kernel<OP, SCMP_SMOOTH_DIV, PT><<<grid, kGroupThreads, 0, stream>>>(
+            a, cpr, segw, nseg, vec);
+        break;
+    case SCMP_SMOOTH_MUL:
+        quant_seg_kernel<OP, SCMP_SMOOTH_MUL, PT><<<grid, kGroupThreads, 0, stream>>>(
+            a, cpr, segw, nseg, vec);
+        break;
+    default:
+        quant_seg_kernel<OP, SCMP_SMOOTH_NONE, PT><<<grid, kGroupThreads, 0, stream>>>(
+            a, cpr, segw, nseg, vec);
+        break;
+    }
+}
+
+// One-row groups with column segments: the row (up to 16384 columns) in registers.
+static int quantize_segments(const scmp_quant_args &a, int64_t segw, int64_t nseg,
+                             hipStream_t stream) {
+    const int cpr = (int)cdiv(a.cols, 4);
+    const bool vec = (a.ld % 4 == 0) && (((uintptr_t)a.x & 15) == 0) &&
+                     (a.smooth_mode == SCMP_SMOOTH_NONE || ((uintptr_t)a.smooth & 15) == 0);
+    const bool small = cpr <= 4 * kGroupThreads;
+    switch (a.variant) {
+    case SCMP_Q_GROUP_SYM:
+        if (small) launch_seg_pt<QOP_DIV, 4>(a, cpr, (int)segw, (int)nseg, vec, stream);
+        else launch_seg_pt<QOP_DIV, kMaxChunks>(a, cpr, (int)segw, (int)nseg, vec, stream);
+        break;
+    case SCMP_Q_GROUP_ASYM:
+        if (small) launch_seg_pt<QOP_DIVZP, 4>(a, cpr, (int)segw, (int)nseg, vec, stream);
+        else launch_seg_pt<QOP_DIVZP, kMaxChunks>(a, cpr, (int)segw, (int)nseg, vec, stream);
+        break;
+    default:
+        if (small) launch_seg_pt<QOP_MUL, 4>(a, cpr, (int)segw, (int)nseg, vec, stream);
+        else launch_seg_pt<QOP_MUL, kMaxChunks>(a, cpr, (int)segw, (int)nseg, vec, stream);
+        break;
+    }
+    SCMP_LAUNCH_CHECK("scmp_quantize/segments");
+    if (a.code) {
+        const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+        if (a.code_rows > cbr) {
+            const int64_t total = (a.code_rows - cbr) * a.code_ld * (a.rows / cbr);
+            int64_t blocks = cdiv(total, 256);
+            if (blocks > 4096) blocks = 4096;
+            zero_code_rows_kernel<<<blocks, 256, 0, stream>>>(a.code, a.code_ld, a.code_rows,
+                                                              cbr, a.rows / cbr);
+            SCMP_LAUNCH_CHECK("scmp_quantize/pad");
+        }
+    }
+    return SCMP_OK;
+}
+
 // One workgroup per row group, instantiated for the variant's element operation, the
 // smoothing mode and the register-held chunk count (4: rows up to 4096 columns; 16).
 template <int OP, int PT>
@@ -695,6 +865,9 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
     if (!host && !tensor && nseg == 1 && G <= kGroupMaxRows && G * a.cols <= (1 << 22) &&
         (!a.code || a.code_ld % 4 == 0))
         return quantize_groups(a, G, stream);
+    if (!host && !tensor && nseg > 1 && G == 1 && nseg <= kMaxSegs && segw % 4 == 0 &&
+        a.cols <= 4 * kGroupThreads * kMaxChunks && (!a.code || a.code_ld % 4 == 0))
+        return quantize_segments(a, segw, nseg, stream);
     if (!host) {
         stats_init_kernel<<<cdiv(2 * nunits, 256), 256, 0, stream>>>(stats, 2 * nunits);
         SCMP_LAUNCH_CHECK("scmp_quantize/init");
