@@ -55,6 +55,16 @@ int scmp_rng_lfsr(int length, int64_t seed, uint64_t taps_mask, int64_t n, int32
 int scmp_rng_expand(const int32_t *base, int64_t n, const int32_t *src, const int32_t *perm,
                     int p, int D, int32_t *out, hipStream_t stream);
 
+/* LFSR tap-set search for an n_bits register (2 <= n_bits <= SCMP_LFSR_SEARCH_MAX_BITS):
+ * distinct[i] = number of distinct states the right-shift LFSR with tap bit mask masks[i]
+ * visits from seed 1 before its first repeat (a tap set is maximal-length when this is
+ * 2^n_bits - 1). One device thread per candidate (Brent cycle detection, O(1) state).
+ * Replaces _is_maximal_length and the enumeration loop of search_taps,
+ * scmp_kernels/sc/lfsr_taps.py:35-111. */
+#define SCMP_LFSR_SEARCH_MAX_BITS 20
+int scmp_lfsr_search(int n_bits, const uint32_t *masks, int64_t count, uint32_t *distinct,
+                     hipStream_t stream);
+
 /* Prefix / Owen XOR / rescale: out[d, t] for t < L from r[d, t] (row length full).
  * masks: per-d XOR masks or NULL (Owen off). R == 2^p: XOR only when L < full.
  * Otherwise XOR when scramble_rescale, then floor(v * R / 2^p).

@@ -60,6 +60,27 @@ EXPORT void orc_lfsr(int length, int64_t seed, const int32_t *taps, int ntaps, i
     }
 }
 
+/* Maximal-length check of an LFSR tap set, scmp_kernels/sc/lfsr_taps.py:99-111: step the
+ * register from seed 1 for up to period + 1 cycles, recording the values seen; at the first
+ * value seen twice return the number of distinct values (the reference compares it with
+ * 2^n - 1), else the number recorded. Visited set: a 2^n-bit map (n <= 24). */
+EXPORT int64_t orc_lfsr_distinct(int n, const int32_t *taps, int ntaps) {
+    const int64_t period = ((int64_t)1 << n) - 1;
+    uint8_t *seen = (uint8_t *)calloc((size_t)(((int64_t)1 << n) + 7) / 8, 1);
+    int64_t reg = 1, count = 0;
+    for (int64_t i = 0; i < period + 1; ++i) {
+        const int64_t val = reg;
+        int64_t x = 0;
+        for (int t = 0; t < ntaps; ++t) x ^= (reg >> taps[t]) & 1;
+        reg = (reg >> 1) | (x << (n - 1));
+        if (seen[val >> 3] & (1u << (val & 7))) break;
+        seen[val >> 3] |= (uint8_t)(1u << (val & 7));
+        ++count;
+    }
+    free(seen);
+    return count;
+}
+
 /* Bit permutation, scmp_kernels/sc/sng.py:15-29: output bit i = input bit perm[i]. */
 EXPORT void orc_scramble(const int32_t *seq, int64_t n, const int32_t *perm, int plen,
                          int32_t *out) {

@@ -90,6 +90,28 @@ def lfsr_sequence(length: int, seed: int, taps: list, n: int) -> np.ndarray:
     return out
 
 
+def lfsr_distinct_states(taps: list, n: int) -> int:
+    """Distinct register values from seed 1 before the first repeat, capped at 2^n
+    (scmp_kernels/sc/lfsr_taps.py:99-111); a tap set is maximal when this is 2^n - 1."""
+    t = np.asarray(taps, dtype=np.int32)
+    f = lib().orc_lfsr_distinct
+    f.restype = ctypes.c_int64
+    return int(f(ctypes.c_int(n), _p(t), ctypes.c_int(len(t))))
+
+
+def lfsr_search(n: int) -> list:
+    """search_taps, scmp_kernels/sc/lfsr_taps.py:35-96: every maximal tap set, MSB plus an
+    odd number of lower positions, in itertools.combinations order by tap count."""
+    from itertools import combinations
+    out = []
+    for n_taps in range(2, n + 1, 2):
+        for combo in combinations(range(n - 1), n_taps - 1):
+            taps = sorted([n - 1] + list(combo), reverse=True)
+            if lfsr_distinct_states(taps, n) == 2 ** n - 1:
+                out.append(taps)
+    return out
+
+
 def true_random_sequence(length: int, seed: int, n: int) -> np.ndarray:
     """scmp_kernels/sc/rng.py:80-113 (Python's Mersenne Twister, randint(0, 2^len - 1))."""
     r = random.Random(seed)

@@ -27,6 +27,7 @@ SMOOTH_NONE, SMOOTH_DIV, SMOOTH_MUL = 0, 1, 2
 CODE_NONE, CODE_THERMO, CODE_Q = 0, 1, 2
 EPI_INT, EPI_ROWCOL, EPI_SCALAR, EPI_HEAD, EPI_ZP_ROWCOL, EPI_ZP_SCALAR = range(6)
 GEMM_MFMA, GEMM_VALU, GEMM_MFMA_FP4 = 0, 1, 2
+LFSR_SEARCH_MAX_BITS = 20          # SCMP_LFSR_SEARCH_MAX_BITS
 
 
 class QuantArgs(ctypes.Structure):
@@ -67,7 +68,7 @@ class GemmArgs(ctypes.Structure):
 
 EXPORTS = [
     "scmp_abi_version", "scmp_last_error", "scmp_rng_sobol", "scmp_rng_lfsr",
-    "scmp_rng_expand", "scmp_rng_prepare", "scmp_build_stream_tables",
+    "scmp_rng_expand", "scmp_rng_prepare", "scmp_lfsr_search", "scmp_build_stream_tables",
     "scmp_quant_workspace_bytes", "scmp_quantize", "scmp_sc_gemm", "scmp_build_bitlut",
     "scmp_build_fp4_lut", "scmp_sc_gemm_workspace_bytes",
 ]
@@ -94,6 +95,7 @@ def load(path: str = LIB_PATH):
         lib.scmp_rng_sobol.argtypes = [c_int, c_vp, c_i64, c_vp, c_vp]
         lib.scmp_rng_lfsr.argtypes = [c_int, c_i64, ctypes.c_uint64, c_i64, c_vp, c_vp]
         lib.scmp_rng_expand.argtypes = [c_vp, c_i64, c_vp, c_vp, c_int, c_int, c_vp, c_vp]
+        lib.scmp_lfsr_search.argtypes = [c_int, c_vp, c_i64, c_vp, c_vp]
         lib.scmp_rng_prepare.argtypes = [c_vp, c_int, c_int, c_int, c_int, c_int, c_vp, c_int,
                                          c_vp, c_vp]
         lib.scmp_build_stream_tables.argtypes = [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int,

@@ -54,6 +54,47 @@ __global__ void lfsr_kernel(int length, int64_t seed, uint64_t taps, int64_t n, 
     }
 }
 
+// Maximal-length test of Fibonacci LFSR tap sets, one candidate per thread. The state
+// sequence from seed 1 (s_{k+1} = (s_k >> 1) | (parity(s_k & mask) << (n - 1))) is
+// eventually periodic; Brent's cycle detection finds its period lam and pre-period mu with
+// O(mu + lam) steps and O(1) state. mu + lam is the number of distinct states before the
+// first repeat; _is_maximal_length (scmp_kernels/sc/lfsr_taps.py:99-111) accepts a tap set
+// when that number equals the expected period 2^n - 1. Every loop is bounded by the 2^n
+// states of the register.
+__device__ __forceinline__ uint32_t lfsr_next(uint32_t x, uint32_t mask, int n) {
+    return (x >> 1) | ((uint32_t)(__builtin_popcount(x & mask) & 1) << (n - 1));
+}
+
+__global__ void lfsr_distinct_kernel(int n, const uint32_t *masks, int64_t count,
+                                     uint32_t *distinct) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const uint32_t mask = masks[i];
+    const uint32_t x0 = 1u;
+    // Brent: lam = period
+    uint32_t power = 1, lam = 1;
+    uint32_t tort = x0, hare = lfsr_next(x0, mask, n);
+    while (tort != hare) {
+        if (power == lam) {
+            tort = hare;
+            power <<= 1;
+            lam = 0;
+        }
+        hare = lfsr_next(hare, mask, n);
+        ++lam;
+    }
+    // mu = first index of the cycle: advance one pointer lam steps, then both together
+    tort = hare = x0;
+    for (uint32_t k = 0; k < lam; ++k) hare = lfsr_next(hare, mask, n);
+    uint32_t mu = 0;
+    while (tort != hare) {
+        tort = lfsr_next(tort, mask, n);
+        hare = lfsr_next(hare, mask, n);
+        ++mu;
+    }
+    distinct[i] = mu + lam;
+}
+
 __global__ void expand_kernel(const int32_t *base, int64_t n, const int32_t *src,
                               const int32_t *perm, int p, int D, int32_t *out) {
     int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -218,6 +259,19 @@ int scmp_rng_lfsr(int length, int64_t seed, uint64_t taps_mask, int64_t n, int32
     if (n == 0) return SCMP_OK;
     lfsr_kernel<<<1, 1, 0, stream>>>(length, seed, taps_mask, n, out);
     SCMP_LAUNCH_CHECK("scmp_rng_lfsr");
+    return SCMP_OK;
+}
+
+int scmp_lfsr_search(int n_bits, const uint32_t *masks, int64_t count, uint32_t *distinct,
+                     hipStream_t stream) {
+    SCMP_REQUIRE(n_bits >= 2 && n_bits <= SCMP_LFSR_SEARCH_MAX_BITS,
+                 "scmp_lfsr_search: n_bits=%d out of range [2, %d]", n_bits,
+                 SCMP_LFSR_SEARCH_MAX_BITS);
+    SCMP_REQUIRE(masks && distinct && count >= 0, "scmp_lfsr_search: bad arguments");
+    if (count == 0) return SCMP_OK;
+    lfsr_distinct_kernel<<<cdiv(count, 256), 256, 0, stream>>>(n_bits, masks, count,
+                                                               distinct);
+    SCMP_LAUNCH_CHECK("scmp_lfsr_search");
     return SCMP_OK;
 }
 
