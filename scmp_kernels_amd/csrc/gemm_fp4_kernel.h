@@ -139,11 +139,19 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     const uint8_t *glut = (const uint8_t *)P.lut;
     const int D = P.D;
 
-    auto load_codes = [&](uint2 (&c)[NR], int g) __attribute__((always_inline)) {
+    // With per-d table classes, lane l also loads the class of inner dimension 8g + (l & 7)
+    // of the group into cls; a unit takes its d's class from that lane (v_readlane), so the
+    // class costs no memory wait inside the loop.
+    const int lane8 = (int)(threadIdx.x & 7);
+    auto load_codes = [&](uint2 (&c)[NR], int &cls, int g) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BA; ++i) c[i] = *(const uint2 *)(pa[i] + 8 * g);
 #pragma unroll
         for (int j = 0; j < BB; ++j) c[BA + j] = *(const uint2 *)(pb[j] + 8 * g);
+        if (LUTSRC != LUT_LDS) {
+            const int d = 8 * g + lane8;
+            cls = d < D ? P.d_class[d] : 0;
+        }
     };
     // code byte of inner dimension dl (0..7, a compile-time constant) of row r
     auto code_of = [](const uint2 (&c)[NR], int r, int dl) __attribute__((always_inline)) {
@@ -151,8 +159,8 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     };
 
     // load unit `unit` of the group whose first d is dg (codes in c) into F
-    auto stage = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&c)[NR], int unit, int dg)
-        __attribute__((always_inline)) {
+    auto stage = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&c)[NR], int cls8, int unit,
+                     int dg) __attribute__((always_inline)) {
         const int dl = JPF == 32 ? 2 * unit + h : unit / SPD;    // d within the group
         const int koff = (JPF == 32 ? 0 : 16 * h) + 32 * KSU * (unit % SPD);
 #pragma unroll
@@ -163,8 +171,14 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         }
         const uint8_t *base = sB;
         if (LUTSRC != LUT_LDS) {
-            const int d = dg + dl;
-            const int cls = d < D ? P.d_class[d] : 0;
+            int cls;
+            if (JPF == 32) {                     // the lane halves take d = 2 unit + h
+                const int c0 = __builtin_amdgcn_readlane(cls8, 2 * unit);
+                const int c1 = __builtin_amdgcn_readlane(cls8, 2 * unit + 1);
+                cls = h ? c1 : c0;
+            } else {
+                cls = __builtin_amdgcn_readlane(cls8, unit / SPD);
+            }
             base = LUTSRC == LUT_GLOBAL ? glut + (int64_t)cls * 256 * ROWB : sB + cls * TAB;
         }
 #pragma unroll
@@ -193,12 +207,12 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     // one group: its units from `cur`; the last unit stages unit 0 of the next group from
     // `nxt` and refills `cur` with the group after that (clamped to the last group of the
     // range, whose codes are then loaded but never used)
-    auto group = [&](uint2 (&cur)[NR], const uint2 (&nxt)[NR], int g)
-        __attribute__((always_inline)) {
+    auto group = [&](uint2 (&cur)[NR], int &ccur, const uint2 (&nxt)[NR], const int &cnxt,
+                     int g) __attribute__((always_inline)) {
         const int dg = 8 * g;
 #pragma unroll
         for (int uu = 0; uu < UPG; uu += 2) {
-            stage(F1, cur, uu + 1, dg);
+            stage(F1, cur, ccur, uu + 1, dg);
             mma(F0);
             if (SCHED) {
                 interleave_unit<BA * BB * KSU, NR * KSU, 1>();
@@ -206,10 +220,10 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             }
             done(uu, dg);
             if (uu + 2 < UPG) {
-                stage(F0, cur, uu + 2, dg);
+                stage(F0, cur, ccur, uu + 2, dg);
             } else {
-                load_codes(cur, g + 2 < g1 ? g + 2 : g1 - 1);
-                stage(F0, nxt, 0, dg + 8);
+                load_codes(cur, ccur, g + 2 < g1 ? g + 2 : g1 - 1);
+                stage(F0, nxt, cnxt, 0, dg + 8);
             }
             mma(F1);
             if (SCHED) {
@@ -221,17 +235,18 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     };
 
     uint2 cx0[NR], cx1[NR];
-    load_codes(cx0, g0);
-    load_codes(cx1, g0 + 1 < g1 ? g0 + 1 : g1 - 1);
-    stage(F0, cx0, 0, 8 * g0);
+    int cl0 = 0, cl1 = 0;
+    load_codes(cx0, cl0, g0);
+    load_codes(cx1, cl1, g0 + 1 < g1 ? g0 + 1 : g1 - 1);
+    stage(F0, cx0, cl0, 0, 8 * g0);
     // pairs of groups, then an odd last group: the loop body has no branch, so the wait
     // for a buffer's codes at the top of the loop only covers loads a group old
     int g = g0;
     for (; g + 1 < g1; g += 2) {
-        group(cx0, cx1, g);
-        group(cx1, cx0, g + 1);
+        group(cx0, cl0, cx1, cl1, g);
+        group(cx1, cl1, cx0, cl0, g + 1);
     }
-    if (g < g1) group(cx0, cx1, g);
+    if (g < g1) group(cx0, cl0, cx1, cl1, g);
 }
 
 // Balanced schedule: workgroup c of nwg owns work items [first(c), first(c+1)) of W.
