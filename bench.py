@@ -277,14 +277,12 @@ def bench_other(args):
         ra = classify_rows_by_metric(metric, CFG5_LEVELS, [1 / 3] * 3)
         B = sum(len(ra.level_row_indices[L]) * 4096 * 4096 * L for L in CFG5_LEVELS)
         desc = "mixed-level unipolar grouped (G=4), 4096x4096x4096, levels {256,64,16}"
-        Y = torch.empty((4096, 4096), dtype=torch.float32, device=dev)
+        from scmp_kernels_amd.mp import sc_matmul_mixed
 
         def step():
-            for L in CFG5_LEVELS:
-                rows = ra.level_row_indices[L]
-                Y[rows] = sc_matmul(a[rows], b, "per_row", mode="unipolar", group_a=4,
-                                    group_b=4, stoc_len=L, rng_levels=L)
-            return Y
+            # Y[rows_L] = sc_matmul(a[rows_L], b, stoc_len=L, rng_levels=L) for every level,
+            # in one call (b quantized once per call, rows read and written in place)
+            return sc_matmul_mixed(a, b, ra, mode="unipolar", group_a=4, group_b=4)
     else:
         raise SystemExit(f"unknown --config {args.config}")
     t, _ = time_steps(step, args.steps, args.warmup)

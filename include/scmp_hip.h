@@ -157,6 +157,9 @@ typedef struct scmp_quant_args {
     float *rowsum;            /* sum of q over the row (exact integers as fp32) */
     /* workspace: >= scmp_quant_workspace_bytes(...) bytes */
     void *workspace;
+    /* input row of each quantized row: row r reads x row row_index[r] (each a valid row of
+     * x), so a caller quantizes a row subset in any order without gathering it; NULL: r */
+    const int64_t *row_index;
 } scmp_quant_args;
 
 int64_t scmp_quant_workspace_bytes(int64_t rows, int64_t cols, int64_t group, int64_t seg);
@@ -219,6 +222,8 @@ typedef struct scmp_gemm_args {
                                   the persistent kernel share tiles between workgroups so
                                   that every CU gets equal work; NULL: whole tiles only */
     int64_t workspace_bytes;
+    const int64_t *row_map;    /* output row of A row n (y / iout row row_map[n], each a valid
+                                  output row): scatters a row subset in place; NULL: n */
 } scmp_gemm_args;
 
 int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream);

@@ -42,6 +42,7 @@ class QuantArgs(ctypes.Structure):
         ("beta16", c_vp), ("beta32", c_vp), ("beta_formula", c_int), ("sign", c_vp),
         ("xint", c_vp), ("out_ld", c_i64), ("scale", c_vp), ("scale64", c_vp), ("inv", c_vp),
         ("zp", c_vp), ("zp64", c_vp), ("rowsum", c_vp), ("workspace", c_vp),
+        ("row_index", c_vp),
     ]
 
 
@@ -62,7 +63,7 @@ class GemmArgs(ctypes.Structure):
         ("bipolar", c_int), ("JP", c_int), ("lut", c_vp), ("d_class", c_vp), ("chunk", c_i64),
         ("epi", Epilogue), ("y", c_vp), ("iout", c_vp), ("ldy", c_i64), ("bsy", c_i64),
         ("impl", c_int), ("bitlut", c_vp), ("tile", c_int), ("nclass", c_int),
-        ("workspace", c_vp), ("workspace_bytes", c_i64),
+        ("workspace", c_vp), ("workspace_bytes", c_i64), ("row_map", c_vp),
     ]
 
 

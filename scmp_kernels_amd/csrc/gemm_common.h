@@ -35,7 +35,13 @@ struct GemmP {
     int nwg;
     float *part;
     int *cnt;
+    const int64_t *row_map;   // output row of A row n (NULL: n)
 };
+
+// Output row of A row n: the caller's row map scatters a row subset in place.
+__device__ __forceinline__ int64_t out_row(const int64_t *row_map, int64_t n) {
+    return row_map ? row_map[n] : n;
+}
 
 // fp32 epilogue of one output element (row n of A, row m of B, batch index) from its
 // exact integer accumulator I, in the operation order of the reference path that the
@@ -78,7 +84,8 @@ __device__ __forceinline__ float epilogue_value(const scmp_epilogue &E, float I,
 }
 
 int run_epilogue(const int32_t *iin, float *y, int64_t N, int64_t M, int64_t batch,
-                 int64_t ldy, int64_t bsy, const scmp_epilogue &E, hipStream_t stream);
+                 int64_t ldy, int64_t bsy, const scmp_epilogue &E, const int64_t *row_map,
+                 hipStream_t stream);
 
 // FP4 kernel launchers, one translation unit per table width JPF (gemm_fp4_jp*.hip).
 // Non-chunked launches apply the epilogue in the kernel (y, or iout for SCMP_EPI_INT).

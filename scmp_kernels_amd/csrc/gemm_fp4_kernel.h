@@ -390,7 +390,7 @@ sc_gemm_fp4_kernel(GemmP P) {
                     v += __builtin_nontemporal_load(&other[pidx(i, c, rr)]);
                 }
                 if (n < P.N && m < P.M) {
-                    const int64_t o = batch * P.bsy + (int64_t)n * P.ldy + m;
+                    const int64_t o = batch * P.bsy + out_row(P.row_map, n) * P.ldy + m;
                     if (P.epi.kind == SCMP_EPI_INT) P.iout[o] = (int32_t)v;
                     else P.y[o] = epilogue_value(P.epi, v, n, m, batch);
                 }
@@ -480,7 +480,7 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
             for (int r = 0; r < 16; ++r) {
                 const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (n >= P.N) continue;
-                P.y[batch * P.bsy + (int64_t)n * P.ldy + m] = yac[i][c][r];
+                P.y[batch * P.bsy + out_row(P.row_map, n) * P.ldy + m] = yac[i][c][r];
             }
     }
 }

@@ -352,7 +352,7 @@ sc_gemm_mfma_kernel(GemmP P) {
             for (int r = 0; r < 16; ++r) {
                 const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (n >= P.N) continue;
-                const int64_t o = batch * P.bsy + (int64_t)n * P.ldy + m;
+                const int64_t o = batch * P.bsy + out_row(P.row_map, n) * P.ldy + m;
                 if (CHUNKED) {
                     P.y[o] = yac[CHUNKED ? i : 0][CHUNKED ? c : 0][r];
                     continue;
@@ -366,21 +366,22 @@ sc_gemm_mfma_kernel(GemmP P) {
 // fp32 epilogues of the reference paths, applied to the int32 accumulator in place
 // (int8 MFMA and VALU kernels; the FP4 kernel applies them itself).
 __global__ void epilogue_kernel(const int32_t *iin, float *y, int N, int M, int64_t ldy,
-                                int64_t bsy, scmp_epilogue E) {
+                                int64_t bsy, scmp_epilogue E, const int64_t *row_map) {
     const int batch = blockIdx.z;
     for (int n = blockIdx.y; n < N; n += gridDim.y)
     for (int m = blockIdx.x * blockDim.x + threadIdx.x; m < M; m += gridDim.x * blockDim.x) {
-        const int64_t o = batch * bsy + (int64_t)n * ldy + m;
+        const int64_t o = batch * bsy + out_row(row_map, n) * ldy + m;
         y[o] = epilogue_value(E, (float)iin[o], n, m, batch);
     }
 }
 
 int run_epilogue(const int32_t *iin, float *y, int64_t N, int64_t M, int64_t batch,
-                 int64_t ldy, int64_t bsy, const scmp_epilogue &E, hipStream_t stream) {
+                 int64_t ldy, int64_t bsy, const scmp_epilogue &E, const int64_t *row_map,
+                 hipStream_t stream) {
     int64_t bx = cdiv(M, 256);
     if (bx > 64) bx = 64;
     dim3 grid((unsigned)bx, (unsigned)(N < 32768 ? N : 32768), (unsigned)batch);
-    epilogue_kernel<<<grid, 256, 0, stream>>>(iin, y, (int)N, (int)M, ldy, bsy, E);
+    epilogue_kernel<<<grid, 256, 0, stream>>>(iin, y, (int)N, (int)M, ldy, bsy, E, row_map);
     SCMP_LAUNCH_CHECK("scmp_sc_gemm(epilogue)");
     return SCMP_OK;
 }
@@ -475,6 +476,7 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     P.chunk = chunked ? (int)a.chunk : 0;
     P.lut = a.lut; P.d_class = a.d_class; P.bipolar = a.bipolar;
     P.epi = a.epi; P.y = a.y; P.ldy = a.ldy; P.bsy = a.bsy;
+    P.row_map = a.row_map;
     P.tilesA = 0;
     P.nclass = a.nclass;
     if (a.impl == SCMP_GEMM_MFMA_FP4) {
@@ -489,5 +491,6 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     const int rc = perclass ? launch_pc<true>(P, a.batch, a.JP, a.tile, chunked, stream)
                             : launch_pc<false>(P, a.batch, a.JP, a.tile, chunked, stream);
     if (rc != SCMP_OK || chunked || a.epi.kind == SCMP_EPI_INT) return rc;
-    return run_epilogue(P.iout, a.y, a.N, a.M, a.batch, a.ldy, a.bsy, a.epi, stream);
+    return run_epilogue(P.iout, a.y, a.N, a.M, a.batch, a.ldy, a.bsy, a.epi, a.row_map,
+                        stream);
 }

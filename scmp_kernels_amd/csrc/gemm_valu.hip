@@ -20,7 +20,8 @@ __global__ void __launch_bounds__(256)
 sc_gemm_valu_kernel(const uint8_t *ca, int64_t lda, int64_t bsa, const uint8_t *cb,
                     int64_t ldb, int64_t bsb, int N, int M, int D, int JP, int bipolar,
                     const uint32_t *bitlut, const int32_t *d_class, scmp_epilogue E,
-                    float *y, int32_t *iout, int64_t ldy, int64_t bsy, int tilesA) {
+                    float *y, int32_t *iout, int64_t ldy, int64_t bsy, int tilesA,
+                    const int64_t *row_map) {
     __shared__ uint32_t sbits[256 * 2 * W];
     __shared__ uint8_t sa_codes[64][17];
     __shared__ uint8_t sb_codes[64][17];
@@ -88,7 +89,7 @@ sc_gemm_valu_kernel(const uint8_t *ca, int64_t lda, int64_t bsa, const uint8_t *
         for (int c = 0; c < 4; ++c) {
             const int m = b0 + 4 * tx + c;
             if (m >= M) continue;
-            const int64_t o = batch * bsy + (int64_t)n * ldy + m;
+            const int64_t o = batch * bsy + out_row(row_map, n) * ldy + m;
             const int I = acc[i][c];
             if (E.kind == SCMP_EPI_INT) iout[o] = I;
             else y[o] = epilogue_value(E, (float)I, n, m, batch);
@@ -107,7 +108,8 @@ int gemm_valu_launch(const scmp_gemm_args &a, hipStream_t stream) {
     case WW:                                                                                 \
         sc_gemm_valu_kernel<WW><<<grid, 256, 0, stream>>>(                                   \
             a.ca, a.lda, a.bsa, a.cb, a.ldb, a.bsb, (int)a.N, (int)a.M, (int)a.D, a.JP,      \
-            a.bipolar, a.bitlut, a.d_class, a.epi, a.y, a.iout, a.ldy, a.bsy, tilesA);       \
+            a.bipolar, a.bitlut, a.d_class, a.epi, a.y, a.iout, a.ldy, a.bsy, tilesA,        \
+            a.row_map);                                                                      \
         break;
     switch (W) {
         SCMP_VALU_CASE(1)

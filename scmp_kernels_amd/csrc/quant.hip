@@ -29,8 +29,13 @@ __device__ __forceinline__ float float_of_key(uint32_t k) {
     return __uint_as_float(b);
 }
 
+// First element of quantized row r: the caller's row index picks the input row.
+__device__ __forceinline__ const float *x_row(const scmp_quant_args &a, int64_t r) {
+    return a.x + (a.row_index ? a.row_index[r] : r) * a.ld;
+}
+
 __device__ __forceinline__ float load_x(const scmp_quant_args &a, int64_t r, int64_t c) {
-    float v = a.x[r * a.ld + c];
+    float v = x_row(a, r)[c];
     if (a.smooth_mode == SCMP_SMOOTH_DIV) v = __fdiv_rn(v, a.smooth[c]);
     else if (a.smooth_mode == SCMP_SMOOTH_MUL) v = __fmul_rn(v, a.smooth[c]);
     return v;
@@ -305,7 +310,7 @@ __device__ __forceinline__ float rne_quotient(float x, float s, float inv, float
 template <int SM>
 __device__ __forceinline__ void load_chunk4(const scmp_quant_args &a, int64_t r, int c,
                                             bool vec, float (&v)[4]) {
-    const float *row = a.x + r * a.ld;
+    const float *row = x_row(a, r);
     if (vec && c + 4 <= a.cols) {
         const float4 x4 = *(const float4 *)(row + c);
         v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;

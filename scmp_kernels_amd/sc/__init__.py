@@ -4,8 +4,11 @@ scmp_kernels/sc/__init__.py:20-27).
 * ``sc_matmul`` — unified granularity dispatcher.
 * ``clear_rng_cache`` — drop cached RNG sequences and stream tables.
 * ``det_kernel_tuning`` — re-entrant context manager (API compatibility).
+* ``prepare_weight`` / ``PreparedWeight`` — the per_row weight quantized once (no
+  counterpart in the reference, which re-quantizes the weight on every call).
 """
 from .matmul import sc_matmul
-from .kernels import clear_rng_cache, det_kernel_tuning
+from .kernels import PreparedWeight, clear_rng_cache, det_kernel_tuning, prepare_weight
 
-__all__ = ["sc_matmul", "clear_rng_cache", "det_kernel_tuning"]
+__all__ = ["sc_matmul", "clear_rng_cache", "det_kernel_tuning", "prepare_weight",
+           "PreparedWeight"]

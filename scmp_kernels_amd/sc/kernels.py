@@ -108,10 +108,14 @@ def quantize(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, *, grou
              code: Optional[torch.Tensor] = None, code_kind: int = 0,
              code_batch_rows: int = 0, jtab=None, col_class=None, beta16=None, beta32=None,
              beta_formula: int = 0, sign=None, xint=None, scale=None, scale64=None, inv=None,
-             zp=None, zp64=None, rowsum=None, host_inv: float = 0.0, host_zp: float = 0.0):
-    """One scmp_quantize call on the current stream; outputs are written in place."""
+             zp=None, zp64=None, rowsum=None, host_inv: float = 0.0, host_zp: float = 0.0,
+             row_index=None):
+    """One scmp_quantize call on the current stream; outputs are written in place.
+    row_index (int64 device tensor): quantize rows x[row_index] in that order."""
     x = _rows2d(x)
     rows, cols = x.shape
+    if row_index is not None:
+        rows = int(row_index.numel())
     G = rows if group <= 0 or group > rows else group
     a = _lib.QuantArgs()
     a.x, a.rows, a.cols, a.ld = x.data_ptr(), rows, cols, x.stride(0)
@@ -130,6 +134,7 @@ def quantize(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, *, grou
     a.zp, a.zp64, a.rowsum = _lib.ptr(zp), _lib.ptr(zp64), _lib.ptr(rowsum)
     ws = _workspace(rows, cols, G, seg, x.device)
     a.workspace = ws.data_ptr()
+    a.row_index = _lib.ptr(row_index)
     _lib.check(_lib.load().scmp_quantize(a, _lib.stream_of(x.device)), "scmp_quantize")
     return ws  # keep the workspace alive until the stream has consumed it
 
@@ -143,7 +148,8 @@ def _gemm_impl() -> Optional[int]:
 
 
 def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.Epilogue",
-            y=None, iout=None, ldy=None, bsy=0, chunk=0, d_class=None, impl=None, tile=None):
+            y=None, iout=None, ldy=None, bsy=0, chunk=0, d_class=None, impl=None, tile=None,
+            row_map=None):
     """scmp_sc_gemm on the current stream. ca / cb are code buffers (batch, rows_pad, ld)
     or (rows_pad, ld)."""
     g = _lib.GemmArgs()
@@ -174,6 +180,7 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
     g.ldy = ldy if ldy is not None else M
     g.bsy = bsy
     g.impl = impl
+    g.row_map = _lib.ptr(row_map)
     g.tile = int(os.environ.get("SCMP_GEMM_TILE", "0")) if tile is None else tile
     if g.impl == _lib.GEMM_VALU:
         g.bitlut = tabs.bitlut(stream).data_ptr()
@@ -230,6 +237,94 @@ def _to_gpu(a: torch.Tensor, b: torch.Tensor):
 
 
 # -------------------------------------------------------------------------------------
+# Prepared weights: the B operand of the per_row path quantized once
+# -------------------------------------------------------------------------------------
+
+class PreparedWeight:
+    """The B operand of the 2-D per_row path, quantized once: GEMM codes (the quantized
+    integers as bytes), per-row scales and, for unipolar, zero-points and row sums. The
+    codes do not depend on stoc_len, rng_levels or the RNG config, so one prepared weight
+    serves every stream length (e.g. every level of a mixed-precision assignment).
+    ``smooth_scales`` is the SmoothQuant vector baked in (b * s), or None."""
+
+    def __init__(self, codes, scale, zp, rowsum, *, M, D, mode, sc_prec, group_b,
+                 smooth_scales, device):
+        self.codes, self.scale, self.zp, self.rowsum = codes, scale, zp, rowsum
+        self.M, self.D, self.mode, self.sc_prec, self.group_b = M, D, mode, sc_prec, group_b
+        self.smooth_scales = smooth_scales
+        self.device = device
+
+    @property
+    def shape(self):
+        return (self.M, self.D)
+
+    def check(self, D: int, mode: str, sc_prec: int, group_b: int, smooth_scales):
+        """ValueError unless this weight was prepared for these sc_matmul arguments."""
+        if D != self.D:
+            raise ValueError(f"sc_matmul: prepared weight has D={self.D}, a has D={D}")
+        if (mode, sc_prec, group_b) != (self.mode, self.sc_prec, self.group_b):
+            raise ValueError(
+                f"sc_matmul: prepared weight was quantized for mode={self.mode!r}, "
+                f"sc_prec={self.sc_prec}, group_b={self.group_b}; the call asks for "
+                f"mode={mode!r}, sc_prec={sc_prec}, group_b={group_b}")
+        mine = self.smooth_scales
+        if (mine is None) != (smooth_scales is None):
+            raise ValueError("sc_matmul: smooth_scales must be the vector the weight was "
+                             "prepared with (or None for both)")
+        if mine is not None and smooth_scales is not mine and not torch.equal(
+                smooth_scales.to(device=mine.device, dtype=mine.dtype), mine):
+            raise ValueError("sc_matmul: smooth_scales differ from the vector the weight "
+                             "was prepared with")
+
+
+@torch.no_grad()
+def prepare_weight(b: torch.Tensor, *, mode: str = "bipolar", sc_prec: int = 8,
+                   group_b: int = 1, smooth_scales: Optional[torch.Tensor] = None
+                   ) -> PreparedWeight:
+    """Quantize the weight ``b`` (M, D) of the per_row path once, with the grouped
+    quantizer that _sc_matmul_per_row applies to b (scmp_kernels/sc/kernels.py:1661-1707),
+    SmoothQuant's ``b * s`` folded into the load (scmp_kernels/quant/smoothquant.py:130-147).
+    ``sc_matmul(a, w, "per_row", ...)`` then quantizes only ``a``."""
+    if mode not in ("bipolar", "unipolar"):
+        raise ValueError(f"Unknown mode: {mode}")
+    if not 1 <= sc_prec <= 8:
+        raise ValueError(f"sc_matmul: sc_prec={sc_prec} outside [1, 8]")
+    if b.dim() != 2:
+        raise ValueError(f"prepare_weight: expected a 2-D weight, got {b.dim()}-D")
+    if not b.is_cuda:
+        if not torch.cuda.is_available():
+            raise RuntimeError("scmp_kernels_amd: the SC kernels run on the GPU; got a CPU "
+                               "weight and no GPU is available")
+        b = b.cuda()
+    dev = b.device
+    M, D = b.shape
+    s = None
+    if smooth_scales is not None:
+        from ..quant.smoothquant import _check_smoothing_vector
+        _check_smoothing_vector(smooth_scales, D, names=("b",))
+        s = smooth_scales.to(device=dev, dtype=torch.float32).contiguous()
+    cb = _codes(M, D, dev)
+    sb = torch.empty(M, dtype=torch.float32, device=dev)
+    zb = rb = None
+    with torch.cuda.device(dev):
+        if mode == "bipolar":
+            Q = 2 ** (sc_prec - 1) - 1
+            ws = quantize(b, _lib.Q_GROUP_SYM, Q, 2 ** sc_prec, group=group_b, smooth=s,
+                          smooth_mode=_lib.SMOOTH_MUL if s is not None else 0, code=cb,
+                          code_kind=_lib.CODE_Q, scale=sb)
+        else:
+            Q = 2 ** sc_prec - 1
+            zb = torch.empty(M, dtype=torch.float32, device=dev)
+            rb = torch.empty(M, dtype=torch.float32, device=dev)
+            ws = quantize(b, _lib.Q_GROUP_ASYM, Q, 2 ** sc_prec, group=group_b, smooth=s,
+                          smooth_mode=_lib.SMOOTH_MUL if s is not None else 0, code=cb,
+                          code_kind=_lib.CODE_Q, scale=sb, zp=zb, rowsum=rb)
+    del ws
+    return PreparedWeight(cb, sb, zb, rb, M=M, D=D, mode=mode, sc_prec=sc_prec,
+                          group_b=group_b, smooth_scales=smooth_scales, device=dev)
+
+
+# -------------------------------------------------------------------------------------
 # per_row, 2-D  (scmp_kernels/sc/kernels.py:1574-1707)
 # -------------------------------------------------------------------------------------
 
@@ -238,51 +333,89 @@ def _sc_matmul_per_row(a, b, group_a=1, group_b=1, mode="unipolar", sc_prec=8, c
                        stoc_len=None, rng_levels=None, smooth_scales=None):
     if stoc_len is None:
         stoc_len = 2 ** sc_prec
-    assert a.dim() == 2 and b.dim() == 2, f"Expected 2D, got a:{a.dim()}D b:{b.dim()}D"
+    prepared = isinstance(b, PreparedWeight)
+    assert a.dim() == 2 and (prepared or b.dim() == 2), \
+        f"Expected 2D, got a:{a.dim()}D b:{len(b.shape)}D"
     assert a.shape[1] == b.shape[1], f"Inner dim mismatch: {a.shape[1]} vs {b.shape[1]}"
     if mode not in ("bipolar", "unipolar"):
         raise ValueError(f"Unknown mode: {mode}")
-    a, b, home = _to_gpu(a, b)
-    N, D = a.shape
-    M = b.shape[0]
-    R = _resolve_rng_levels(sc_prec, rng_levels)
-    dev = a.device
-    bip = mode == "bipolar"
-    tabs = _get_tables(config, sc_prec, stoc_len, R, bip, D, dev)
-    ca, cb = _codes(N, D, dev), _codes(M, D, dev)
-    sa = torch.empty(N, dtype=torch.float32, device=dev)
-    sb = torch.empty(M, dtype=torch.float32, device=dev)
-    y = torch.empty((N, M), dtype=torch.float32, device=dev)
-    s_a, m_a = _smooth_args(smooth_scales, "a")
-    s_b, m_b = _smooth_args(smooth_scales, "b")
-    epi = _lib.Epilogue()
-    if bip:
-        Q = 2 ** (sc_prec - 1) - 1
-        w1 = quantize(a, _lib.Q_GROUP_SYM, Q, R, group=group_a, smooth=s_a, smooth_mode=m_a,
-                      code=ca, code_kind=_lib.CODE_THERMO, jtab=tabs.jtab,
-                      col_class=tabs.d_class, scale=sa)
-        w2 = quantize(b, _lib.Q_GROUP_SYM, Q, R, group=group_b, smooth=s_b, smooth_mode=m_b,
-                      code=cb, code_kind=_lib.CODE_Q, scale=sb)
-        epi.kind, epi.c = _lib.EPI_ROWCOL, _inner_scale(Q, stoc_len)
-        epi.sa, epi.sb = sa.data_ptr(), sb.data_ptr()
-        sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, y=y)
+    if prepared:
+        a, home = _to_gpu_one(a, b.device)
+        w = b
     else:
-        Q = 2 ** sc_prec - 1
-        za = torch.empty(N, dtype=torch.float32, device=dev)
-        zb = torch.empty(M, dtype=torch.float32, device=dev)
-        ra = torch.empty(N, dtype=torch.float32, device=dev)
-        rb = torch.empty(M, dtype=torch.float32, device=dev)
-        w1 = quantize(a, _lib.Q_GROUP_ASYM, Q, R, group=group_a, smooth=s_a, smooth_mode=m_a,
-                      code=ca, code_kind=_lib.CODE_THERMO, jtab=tabs.jtab,
-                      col_class=tabs.d_class, scale=sa, zp=za, rowsum=ra)
-        w2 = quantize(b, _lib.Q_GROUP_ASYM, Q, R, group=group_b, smooth=s_b, smooth_mode=m_b,
-                      code=cb, code_kind=_lib.CODE_Q, scale=sb, zp=zb, rowsum=rb)
-        epi.kind, epi.c = _lib.EPI_ZP_ROWCOL, _inner_scale(Q, stoc_len)
-        epi.sa, epi.sb, epi.za, epi.zb = sa.data_ptr(), sb.data_ptr(), za.data_ptr(), zb.data_ptr()
-        epi.suma, epi.sumb, epi.dfloat = ra.data_ptr(), rb.data_ptr(), float(np.float32(D))
-        sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, y=y)
-    del w1, w2
+        a, b, home = _to_gpu(a, b)
+        w = None
+    R = _resolve_rng_levels(sc_prec, rng_levels)
+    y = torch.empty((a.shape[0], b.shape[0]), dtype=torch.float32, device=a.device)
+    _per_row_levels(a, b if w is None else w, [(stoc_len, R, None)], y, group_a=group_a,
+                    group_b=group_b, mode=mode, sc_prec=sc_prec, config=config,
+                    smooth_scales=smooth_scales)
     return y.to(home) if home is not None else y
+
+
+def _to_gpu_one(a: torch.Tensor, device):
+    """a on the prepared weight's device (CPU input: moved there, result moved back)."""
+    home = None
+    if not a.is_cuda:
+        home = a.device
+        a = a.to(device)
+    elif a.device != device:
+        raise ValueError(f"sc_matmul: a is on {a.device}, the prepared weight on {device}")
+    return a, home
+
+
+def _per_row_levels(a, b, levels, y, *, group_a, group_b, mode, sc_prec, config,
+                    smooth_scales):
+    """The 2-D per_row path (scmp_kernels/sc/kernels.py:1574-1707) for one or more stream
+    lengths: ``levels`` is a list of (stoc_len, rng_levels, rows) with rows an int64 device
+    tensor of rows of ``a`` (None: all rows). Each level quantizes a[rows] (read in place
+    through the quantizer's row index, grouped in that order) at its own boundary grid and
+    writes Y[rows] through the GEMM's row map; b (a tensor or a PreparedWeight) is quantized
+    at most once."""
+    dev = a.device
+    D = a.shape[1]
+    bip = mode == "bipolar"
+    Q = 2 ** (sc_prec - 1) - 1 if bip else 2 ** sc_prec - 1
+    s_a, m_a = _smooth_args(smooth_scales, "a")
+    if isinstance(b, PreparedWeight):
+        w = b
+    else:
+        w = prepare_weight(b, mode=mode, sc_prec=sc_prec, group_b=group_b,
+                           smooth_scales=smooth_scales)
+    M = w.M
+    keep = []
+    for stoc_len, R, rows in levels:
+        N = a.shape[0] if rows is None else int(rows.numel())
+        if N == 0:
+            continue
+        tabs = _get_tables(config, sc_prec, stoc_len, R, bip, D, dev)
+        ca = _codes(N, D, dev)
+        sa = torch.empty(N, dtype=torch.float32, device=dev)
+        epi = _lib.Epilogue()
+        epi.c = _inner_scale(Q, stoc_len)
+        epi.sa, epi.sb = sa.data_ptr(), w.scale.data_ptr()
+        if bip:
+            wq = quantize(a, _lib.Q_GROUP_SYM, Q, R, group=group_a, smooth=s_a,
+                          smooth_mode=m_a, code=ca, code_kind=_lib.CODE_THERMO,
+                          jtab=tabs.jtab, col_class=tabs.d_class, scale=sa, row_index=rows)
+            epi.kind = _lib.EPI_ROWCOL
+            keep.append((ca, sa))
+        else:
+            za = torch.empty(N, dtype=torch.float32, device=dev)
+            ra = torch.empty(N, dtype=torch.float32, device=dev)
+            wq = quantize(a, _lib.Q_GROUP_ASYM, Q, R, group=group_a, smooth=s_a,
+                          smooth_mode=m_a, code=ca, code_kind=_lib.CODE_THERMO,
+                          jtab=tabs.jtab, col_class=tabs.d_class, scale=sa, zp=za,
+                          rowsum=ra, row_index=rows)
+            epi.kind = _lib.EPI_ZP_ROWCOL
+            epi.za, epi.zb = za.data_ptr(), w.zp.data_ptr()
+            epi.suma, epi.sumb = ra.data_ptr(), w.rowsum.data_ptr()
+            epi.dfloat = float(np.float32(D))
+            keep.append((ca, sa, za, ra))
+        wg = sc_gemm(ca, w.codes, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, y=y,
+                     ldy=y.stride(0), row_map=rows)
+        keep.append((wq, wg))
+    return keep
 
 
 # -------------------------------------------------------------------------------------

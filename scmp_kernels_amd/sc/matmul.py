@@ -104,6 +104,12 @@ def sc_matmul(
     SmoothQuant vector, ``sc_matmul(a, b, smooth_scales=s) == sc_matmul(a / s, b * s)``.
     sc_prec must lie in [1, 8] (byte operand codes).
     """
+    if isinstance(b, _paths.PreparedWeight):
+        return _sc_matmul_prepared(a, b, granularity, mode=mode, sc_prec=sc_prec,
+                                   stoc_len=stoc_len, chunk_d=chunk_d, group_a=group_a,
+                                   group_b=group_b, rng_levels=rng_levels, config=config,
+                                   halve_bipolar_stoc_len=halve_bipolar_stoc_len,
+                                   smooth_scales=smooth_scales)
     with _device_scope(a, b):
         _check_combination(a, b, granularity, mode, chunk_d)
         if halve_bipolar_stoc_len and mode == "bipolar":
@@ -128,6 +134,41 @@ def sc_matmul(
         if a.dim() == 3:
             return _paths._sc_matmul_per_row_batched(a, b, **groups, **common)
         return _paths._sc_matmul_per_row(a, b, **groups, **common)
+
+
+def _sc_matmul_prepared(a, w, granularity, *, mode, sc_prec, stoc_len, chunk_d, group_a,
+                        group_b, rng_levels, config, halve_bipolar_stoc_len, smooth_scales):
+    """sc_matmul with a weight from ``prepare_weight``: the 2-D per_row path without the
+    weight's quantizer. Results equal sc_matmul(a, b, ...) with the original weight."""
+    if granularity != "per_row" or chunk_d > 0 or a.dim() != 2:
+        raise ValueError("sc_matmul: a prepared weight supports granularity='per_row' with "
+                         f"2-D a and chunk_d=0, got granularity='{granularity}', "
+                         f"chunk_d={chunk_d}, a.dim()={a.dim()}.")
+    if mode not in _VALID_MODES:
+        raise ValueError(f"sc_matmul: unknown mode '{mode}'. Expected one of {_VALID_MODES}.")
+    if halve_bipolar_stoc_len and mode == "bipolar":
+        half = 2 ** (sc_prec - 1)
+        stoc_len = half if stoc_len is None else stoc_len
+        rng_levels = half if rng_levels is None else rng_levels
+    if stoc_len is not None and stoc_len > 2 ** sc_prec:
+        raise ValueError(
+            f"sc_matmul: stoc_len={stoc_len} exceeds 2**sc_prec={2 ** sc_prec}; the RNG "
+            f"sequences are 2**sc_prec long.")
+    smooth = None
+    if smooth_scales is not None:
+        if a.dtype != torch.float32:
+            raise ValueError("sc_matmul: a prepared weight with smooth_scales needs float32 "
+                             "activations")
+        _check_smoothing_vector(smooth_scales, a.shape[-1], names=("a",))
+        smooth = smooth_scales.to(device=w.device, dtype=torch.float32).contiguous()
+        # the weight was prepared with this vector (compared by PreparedWeight.check)
+        if smooth_scales is w.smooth_scales:
+            smooth = w.smooth_scales.to(device=w.device, dtype=torch.float32).contiguous()
+    with torch.cuda.device(w.device):
+        w.check(a.shape[-1], mode, sc_prec, group_b, smooth_scales)
+        return _paths._sc_matmul_per_row(a, w, group_a=group_a, group_b=group_b, mode=mode,
+                                         sc_prec=sc_prec, config=config, stoc_len=stoc_len,
+                                         rng_levels=rng_levels, smooth_scales=smooth)
 
 
 _sc_matmul_impl = sc_matmul
