@@ -120,6 +120,13 @@ def sc_matmul(
             raise ValueError(
                 f"sc_matmul: stoc_len={stoc_len} exceeds 2**sc_prec={2 ** sc_prec}; the RNG "
                 f"sequences are 2**sc_prec long.")
+        if a.shape[-2] == 0 or b.shape[-2] == 0:
+            # no rows on one side: an empty product, nothing to launch
+            lead = a.shape[:-2] if a.dim() == 3 else ()
+            return torch.empty((*lead, a.shape[-2], b.shape[-2]), dtype=torch.float32,
+                               device=a.device)
+        if a.shape[-1] == 0:
+            raise ValueError("sc_matmul: the inner dimension D must be positive")
         a, b, smooth = _smoothing_for_kernels(a, b, smooth_scales)
         common = dict(mode=mode, sc_prec=sc_prec, config=config, stoc_len=stoc_len,
                       rng_levels=rng_levels, smooth_scales=smooth)

@@ -157,3 +157,21 @@ def test_operands_on_different_devices_rejected():
     a = _dev_randn(4, 16)
     with pytest.raises(ValueError, match="same device"):
         sc_matmul(a, a.cpu())
+
+
+@pytest.mark.parametrize("gran,sa,sb,out", [
+    ("per_row", (0, 64), (16, 64), (0, 16)),
+    ("per_row", (8, 64), (0, 64), (8, 0)),
+    ("per_tensor", (0, 32), (5, 32), (0, 5)),
+    ("per_row", (3, 0, 64), (3, 16, 64), (3, 0, 16)),
+])
+def test_empty_operands_give_empty_output(gran, sa, sb, out):
+    """No rows on one side: an empty float32 product on the operands' device, no launch
+    (runs on the CPU too: nothing reaches the GPU)."""
+    y = sc_matmul(torch.zeros(sa), torch.zeros(sb), granularity=gran)
+    assert tuple(y.shape) == out and y.dtype == torch.float32 and y.device.type == "cpu"
+
+
+def test_zero_inner_dimension_rejected():
+    with pytest.raises(ValueError, match="inner dimension"):
+        sc_matmul(torch.zeros(4, 0), torch.zeros(5, 0))
