@@ -10,6 +10,7 @@ typedef char v16c __attribute__((ext_vector_type(16)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 // Launch parameters of the MFMA SC GEMM kernels (passed by value).
 struct GemmP {
@@ -43,44 +44,83 @@ __device__ __forceinline__ int64_t out_row(const int64_t *row_map, int64_t n) {
     return row_map ? row_map[n] : n;
 }
 
-// fp32 epilogue of one output element (row n of A, row m of B, batch index) from its
-// exact integer accumulator I, in the operation order of the reference path that the
-// kind stands for. One IEEE rounding per operation (no contraction).
-__device__ __forceinline__ float epilogue_value(const scmp_epilogue &E, float I, int64_t n,
-                                                int64_t m, int64_t batch) {
-    switch (E.kind) {
-    case SCMP_EPI_ROWCOL: {
-        // fl(fl(I*c) * fl(sa*sb)): sc/kernels.py:248 then :1707 / :1271 / :1894
-        const float raw = __fmul_rn(I, E.c);
-        const float s = __fmul_rn(E.sa[batch * E.sa_batch_stride + n],
-                                  E.sb[batch * E.sb_batch_stride + m]);
-        return __fmul_rn(raw, s);
+// fp32 epilogue of one output element from its exact integer accumulator I, in the
+// operation order of the reference path that the kind stands for. One IEEE rounding per
+// operation (no contraction). The inputs split into row factors (sa, za, suma of row n),
+// column factors (sb, zb, sumb of column m) and tile-uniform values (s, za, zb, t3 of the
+// scalar kinds), so a kernel can load them once per tile instead of once per element.
+struct EpiUniform {
+    float s, za, zb, t3;
+};
+
+__device__ __forceinline__ EpiUniform epi_uniform(const scmp_epilogue &E, int64_t batch) {
+    EpiUniform u = {0.f, 0.f, 0.f, 0.f};
+    if (E.kind == SCMP_EPI_SCALAR) u.s = E.s[0];
+    else if (E.kind == SCMP_EPI_HEAD) u.s = E.s[batch];
+    else if (E.kind == SCMP_EPI_ZP_SCALAR) {
+        u.s = E.s[0];
+        u.za = E.za[0];
+        u.zb = E.zb[0];
+        u.t3 = E.t3[0];
     }
+    return u;
+}
+
+// f[0..2] = sa, za, suma of row n (only those the kind reads)
+__device__ __forceinline__ void epi_row_factors(const scmp_epilogue &E, int64_t n, int64_t batch,
+                                                float (&f)[3]) {
+    const int64_t i = batch * E.sa_batch_stride + n;
+    f[0] = f[1] = f[2] = 0.f;
+    if (E.kind == SCMP_EPI_ROWCOL || E.kind == SCMP_EPI_ZP_ROWCOL) f[0] = E.sa[i];
+    if (E.kind == SCMP_EPI_ZP_ROWCOL) f[1] = E.za[i];
+    if (E.kind == SCMP_EPI_ZP_ROWCOL || E.kind == SCMP_EPI_ZP_SCALAR) f[2] = E.suma[i];
+}
+
+// f[0..2] = sb, zb, sumb of column m (only those the kind reads)
+__device__ __forceinline__ void epi_col_factors(const scmp_epilogue &E, int64_t m, int64_t batch,
+                                                float (&f)[3]) {
+    const int64_t i = batch * E.sb_batch_stride + m;
+    f[0] = f[1] = f[2] = 0.f;
+    if (E.kind == SCMP_EPI_ROWCOL || E.kind == SCMP_EPI_ZP_ROWCOL) f[0] = E.sb[i];
+    if (E.kind == SCMP_EPI_ZP_ROWCOL) f[1] = E.zb[i];
+    if (E.kind == SCMP_EPI_ZP_ROWCOL || E.kind == SCMP_EPI_ZP_SCALAR) f[2] = E.sumb[i];
+}
+
+__device__ __forceinline__ float epilogue_apply(const scmp_epilogue &E, float I, float ra,
+                                                float rz, float rs, float cb, float cz,
+                                                float cs, const EpiUniform &u) {
+    switch (E.kind) {
+    case SCMP_EPI_ROWCOL:  // fl(fl(I*c) * fl(sa*sb)): sc/kernels.py:248 then :1707 / :1271 / :1894
+        return __fmul_rn(__fmul_rn(I, E.c), __fmul_rn(ra, cb));
     case SCMP_EPI_SCALAR:  // sc/kernels.py:1204 (the scale product is a float64 value)
-        return __fmul_rn(__fmul_rn(I, E.c), E.s[0]);
+        return __fmul_rn(__fmul_rn(I, E.c), u.s);
     case SCMP_EPI_HEAD:    // sc/kernels.py:430-432
-        return __fmul_rn(I, __fmul_rn(E.c, E.s[batch]));
+        return __fmul_rn(I, __fmul_rn(E.c, u.s));
     case SCMP_EPI_ZP_ROWCOL: {  // sc/kernels.py:1699-1707
-        const int64_t na = batch * E.sa_batch_stride + n;
-        const int64_t mb = batch * E.sb_batch_stride + m;
         float raw = __fmul_rn(I, E.c);
-        const float za = E.za[na], zb = E.zb[mb];
-        const float t1 = __fmul_rn(-zb, E.suma[na]);
-        const float t2 = __fmul_rn(za, E.sumb[mb]);
-        const float t3 = __fmul_rn(__fmul_rn(E.dfloat, za), zb);
-        const float corr = __fadd_rn(__fsub_rn(t1, t2), t3);
-        raw = __fadd_rn(raw, corr);
-        return __fmul_rn(raw, __fmul_rn(E.sa[na], E.sb[mb]));
+        const float t1 = __fmul_rn(-cz, rs);
+        const float t2 = __fmul_rn(rz, cs);
+        const float t3 = __fmul_rn(__fmul_rn(E.dfloat, rz), cz);
+        raw = __fadd_rn(raw, __fadd_rn(__fsub_rn(t1, t2), t3));
+        return __fmul_rn(raw, __fmul_rn(ra, cb));
     }
     default: {  // SCMP_EPI_ZP_SCALAR, sc/kernels.py:1198-1204
         float raw = __fmul_rn(I, E.c);
-        const float t1 = __fmul_rn(-E.zb[0], E.suma[batch * E.sa_batch_stride + n]);
-        const float t2 = __fmul_rn(E.za[0], E.sumb[batch * E.sb_batch_stride + m]);
-        const float corr = __fadd_rn(__fsub_rn(t1, t2), E.t3[0]);
-        raw = __fadd_rn(raw, corr);
-        return __fmul_rn(raw, E.s[0]);
+        const float t1 = __fmul_rn(-u.zb, rs);
+        const float t2 = __fmul_rn(u.za, cs);
+        raw = __fadd_rn(raw, __fadd_rn(__fsub_rn(t1, t2), u.t3));
+        return __fmul_rn(raw, u.s);
     }
     }
+}
+
+// The epilogue of one element, loading its factors (kernels without per-tile staging).
+__device__ __forceinline__ float epilogue_value(const scmp_epilogue &E, float I, int64_t n,
+                                                int64_t m, int64_t batch) {
+    float r[3], c[3];
+    epi_row_factors(E, n, batch, r);
+    epi_col_factors(E, m, batch, c);
+    return epilogue_apply(E, I, r[0], r[1], r[2], c[0], c[1], c[2], epi_uniform(E, batch));
 }
 
 int run_epilogue(const int32_t *iin, float *y, int64_t N, int64_t M, int64_t batch,

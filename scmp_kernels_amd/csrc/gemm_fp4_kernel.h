@@ -48,6 +48,8 @@ enum { LUT_LDS = 0, LUT_LDS_CLASSES = 1, LUT_GLOBAL = 2 };
 
 // floats of the per-wave epilogue staging area: one 32 x 32 block, rows padded to 33
 constexpr int kStageFloats = 32 * 33;
+// floats of the per-tile epilogue factors: 3 per row and 3 per column of a 256 x 256 tile
+constexpr int kFactorFloats = 6 * 256;
 
 // accelerator complex dies (XCDs) of an MI355X; workgroup i runs on XCD i mod 8
 constexpr int kXcds = 8;
@@ -276,6 +278,10 @@ sc_gemm_fp4_kernel(GemmP P) {
     uint8_t *sA = smem;                                  // thermometer table
     uint8_t *sB = smem + Fp4Geom<JPF>::TAB;              // stream table(s)
     float *stg_all = (float *)(smem + ((tabs + 15) & ~15));
+    constexpr int TR = WA * BA * 32, TC = WB * BB * 32;   // tile rows / columns
+    static_assert(TR <= 256 && TC <= 256, "epilogue factor area holds 256 rows / columns");
+    float *s_rowf = stg_all + NW * kStageFloats;         // [3][256] sa, za, suma
+    float *s_colf = s_rowf + 3 * 256;                    // [3][256] sb, zb, sumb
 
     fp4_load_tables<JPF, LUTSRC, NT>(P, sA, sB);
     __syncthreads();
@@ -324,27 +330,10 @@ sc_gemm_fp4_kernel(GemmP P) {
         fp4_accumulate<JPF, BA, BB, LUTSRC, SCHED>(P, sA, sB, pa, pb, g0, g1, h, acc,
                                                     [](int, int) {});
 
-        // Every accumulator block leaves its registers through this wave's LDS staging
-        // area only: it is written there, then read back row-wise (lanes 0-31 / 32-63
-        // take 32 consecutive m of rows 2k / 2k+1), and sink(i, c, rr, col, v) consumes
-        // the value of row rr, column col of block (i, c).
-        auto drain = [&](auto sink) __attribute__((always_inline)) {
-#pragma unroll
-            for (int i = 0; i < BA; ++i)
-#pragma unroll
-                for (int c = 0; c < BB; ++c) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        stg[(8 * (r >> 2) + 4 * h + (r & 3)) * 33 + li] = acc[i][c][r];
-                    __syncthreads();
-#pragma unroll 2
-                    for (int rr = ehalf; rr < 32; rr += 2) sink(i, c, rr, stg[rr * 33 + ecol]);
-                    __syncthreads();
-                }
-        };
-        // offset of (block, row, column) inside a partial-sum slot (row-major blocks)
-        auto pidx = [&](int i, int c, int rr) __attribute__((always_inline)) {
-            return (((wave * BA + i) * BB + c) * 32 + rr) * 32 + ecol;
+        // partial-sum slot layout: block (i, c) of this wave, then lane, then the 16
+        // accumulator registers of the lane (the MFMA layout itself, 64 B per lane)
+        auto pblk = [&](int i, int c) __attribute__((always_inline)) {
+            return (int64_t)((wave * BA + i) * BB + c) * 1024 + lane * 16;
         };
 
         const bool shared = g0 != 0 || g1 != ngroups;
@@ -352,15 +341,23 @@ sc_gemm_fp4_kernel(GemmP P) {
         int64_t cf = 0, cl = -1;
         if (shared) {
             // A tile shared with other workgroups: publish this workgroup's partial sums
-            // (slot 0: its first segment, slot 1: its last one), then count in; the
-            // workgroup that completes the count finishes the tile.
+            // (slot 0: its first segment, slot 1: its last one) straight from the
+            // accumulators, then count in; the workgroup that completes the count
+            // finishes the tile.
             const int64_t tfirst = t * ngroups;
             cf = sched_owner(tfirst, W, nwg);
             cl = sched_owner(tfirst + ngroups - 1, W, nwg);
             float *mine = P.part + fp4_slot(c_self, t, W, nwg, ngroups) * (int64_t)TILE_FLOATS;
-            drain([&](int i, int c, int rr, float v) __attribute__((always_inline)) {
-                mine[pidx(i, c, rr)] = v;
-            });
+#pragma unroll
+            for (int i = 0; i < BA; ++i)
+#pragma unroll
+                for (int c = 0; c < BB; ++c) {
+                    v4f *dst = (v4f *)(mine + pblk(i, c));
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        dst[q] = (v4f){acc[i][c][4 * q], acc[i][c][4 * q + 1],
+                                       acc[i][c][4 * q + 2], acc[i][c][4 * q + 3]};
+                }
             // The barrier waits for every wave's stores; one device-scope fence then
             // publishes them (and, for the finisher, makes the others' visible: the L1
             // and L2 invalidation it performs covers the whole CU).
@@ -377,24 +374,90 @@ sc_gemm_fp4_kernel(GemmP P) {
             }
             __syncthreads();
             finish = s_last != 0;
-        }
-
-        if (finish) {
-            // fused epilogue, after adding the other contributors' exact partial sums
-            drain([&](int i, int c, int rr, float v) __attribute__((always_inline)) {
-                const int n = a0 + 32 * i + rr, m = b0 + 32 * c + ecol;
+            if (finish) {
+                // add the other contributors' exact partial sums into the accumulators
+                // (integers below 2^24: exact in any order), all loads of a row of
+                // blocks issued before their adds
                 for (int64_t c2 = cf; c2 <= cl; ++c2) {
                     if (c2 == c_self) continue;
                     const float *other =
                         P.part + fp4_slot(c2, t, W, nwg, ngroups) * (int64_t)TILE_FLOATS;
-                    v += __builtin_nontemporal_load(&other[pidx(i, c, rr)]);
+#pragma unroll
+                    for (int i = 0; i < BA; ++i) {
+                        v4f ov[BB][4];
+#pragma unroll
+                        for (int c = 0; c < BB; ++c)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q)
+                                ov[c][q] = __builtin_nontemporal_load(
+                                    (const v4f *)(other + pblk(i, c)) + q);
+#pragma unroll
+                        for (int c = 0; c < BB; ++c)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) acc[i][c][4 * q + e] += ov[c][q][e];
+                    }
                 }
-                if (n < P.N && m < P.M) {
-                    const int64_t o = batch * P.bsy + out_row(P.row_map, n) * P.ldy + m;
-                    if (P.epi.kind == SCMP_EPI_INT) P.iout[o] = (int32_t)v;
-                    else P.y[o] = epilogue_value(P.epi, v, n, m, batch);
+            }
+        }
+
+        if (finish) {
+            // the tile's epilogue factors, once: row factors of its TR rows and column
+            // factors of its TC columns into LDS, the uniform ones into registers
+            const int tr0 = ta * TR, tc0 = tb * TC;
+            const bool fp32 = P.epi.kind != SCMP_EPI_INT;
+            __syncthreads();          // every wave is past the previous tile's last store
+            if (fp32) {
+                for (int e = tid; e < TR; e += NT) {
+                    float f[3] = {0.f, 0.f, 0.f};
+                    if (tr0 + e < P.N) epi_row_factors(P.epi, tr0 + e, batch, f);
+                    s_rowf[e] = f[0];
+                    s_rowf[256 + e] = f[1];
+                    s_rowf[512 + e] = f[2];
                 }
-            });
+                for (int e = tid; e < TC; e += NT) {
+                    float f[3] = {0.f, 0.f, 0.f};
+                    if (tc0 + e < P.M) epi_col_factors(P.epi, tc0 + e, batch, f);
+                    s_colf[e] = f[0];
+                    s_colf[256 + e] = f[1];
+                    s_colf[512 + e] = f[2];
+                }
+            }
+            const EpiUniform eu = fp32 ? epi_uniform(P.epi, batch) : EpiUniform{0.f, 0.f, 0.f, 0.f};
+            __syncthreads();
+            // fused epilogue: every block leaves the accumulators through this wave's LDS
+            // staging area (written in the MFMA layout, read back row-wise: lanes 0-31 /
+            // 32-63 take 32 consecutive m of rows 2k / 2k+1) and is stored with its fp32
+            // epilogue. Only stores reach global memory here.
+            float *__restrict__ yout = P.y;
+            int32_t *__restrict__ iout = P.iout;
+            const int64_t ybase = batch * P.bsy;
+#pragma unroll
+            for (int i = 0; i < BA; ++i)
+#pragma unroll
+                for (int c = 0; c < BB; ++c) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        stg[(8 * (r >> 2) + 4 * h + (r & 3)) * 33 + li] = acc[i][c][r];
+                    __syncthreads();
+                    const int m = b0 + 32 * c + ecol, mc = m - tc0;
+#pragma unroll 4
+                    for (int rr = ehalf; rr < 32; rr += 2) {
+                        const float v = stg[rr * 33 + ecol];
+                        const int n = a0 + 32 * i + rr, nr = n - tr0;
+                        if (n < P.N && m < P.M) {
+                            const int64_t o = ybase + out_row(P.row_map, n) * P.ldy + m;
+                            if (!fp32)
+                                iout[o] = (int32_t)v;
+                            else
+                                yout[o] = epilogue_apply(P.epi, v, s_rowf[nr], s_rowf[256 + nr],
+                                                         s_rowf[512 + nr], s_colf[mc],
+                                                         s_colf[256 + mc], s_colf[512 + mc], eu);
+                        }
+                    }
+                    __syncthreads();
+                }
         }
         u = t * ngroups + g1;
     }
@@ -516,7 +579,7 @@ static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
     GemmP P = P0;
     auto kern = sc_gemm_fp4_kernel<JPF, BA, BB, WA, WB, LUTSRC, true>;
     const size_t lds = ((fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15) +
-                       (size_t)WA * WB * kStageFloats * sizeof(float);
+                       ((size_t)WA * WB * kStageFloats + kFactorFloats) * sizeof(float);
     int rc = fp4_set_lds(kern, lds);
     if (rc != SCMP_OK) return rc;
     kern<<<dim3((unsigned)P.nwg), 64 * WA * WB, lds, stream>>>(P);
@@ -546,7 +609,7 @@ static int launch_fp4_chunked(const GemmP &P0, int64_t batch, hipStream_t stream
 template <int JPF>
 int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t s) {
     using G = Fp4Geom<JPF>;
-    const int64_t stage = 4 * kStageFloats * (int64_t)sizeof(float);
+    const int64_t stage = (4 * kStageFloats + kFactorFloats) * (int64_t)sizeof(float);
     if (P.d_class == nullptr)
         return chunked ? launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s)
                        : launch_fp4_main<JPF, LUT_LDS>(P, batch, s);
