@@ -86,31 +86,44 @@ __device__ __forceinline__ void epi_col_factors(const scmp_epilogue &E, int64_t 
     if (E.kind == SCMP_EPI_ZP_ROWCOL || E.kind == SCMP_EPI_ZP_SCALAR) f[2] = E.sumb[i];
 }
 
-__device__ __forceinline__ float epilogue_apply(const scmp_epilogue &E, float I, float ra,
-                                                float rz, float rs, float cb, float cz,
-                                                float cs, const EpiUniform &u) {
-    switch (E.kind) {
-    case SCMP_EPI_ROWCOL:  // fl(fl(I*c) * fl(sa*sb)): sc/kernels.py:248 then :1707 / :1271 / :1894
+template <int KIND>
+__device__ __forceinline__ float epilogue_apply_k(const scmp_epilogue &E, float I, float ra,
+                                                  float rz, float rs, float cb, float cz,
+                                                  float cs, const EpiUniform &u) {
+    if constexpr (KIND == SCMP_EPI_ROWCOL) {
+        // fl(fl(I*c) * fl(sa*sb)): sc/kernels.py:248 then :1707 / :1271 / :1894
         return __fmul_rn(__fmul_rn(I, E.c), __fmul_rn(ra, cb));
-    case SCMP_EPI_SCALAR:  // sc/kernels.py:1204 (the scale product is a float64 value)
+    } else if constexpr (KIND == SCMP_EPI_SCALAR) {
+        // sc/kernels.py:1204 (the scale product is a float64 value)
         return __fmul_rn(__fmul_rn(I, E.c), u.s);
-    case SCMP_EPI_HEAD:    // sc/kernels.py:430-432
-        return __fmul_rn(I, __fmul_rn(E.c, u.s));
-    case SCMP_EPI_ZP_ROWCOL: {  // sc/kernels.py:1699-1707
+    } else if constexpr (KIND == SCMP_EPI_HEAD) {
+        return __fmul_rn(I, __fmul_rn(E.c, u.s));           // sc/kernels.py:430-432
+    } else if constexpr (KIND == SCMP_EPI_ZP_ROWCOL) {      // sc/kernels.py:1699-1707
         float raw = __fmul_rn(I, E.c);
         const float t1 = __fmul_rn(-cz, rs);
         const float t2 = __fmul_rn(rz, cs);
         const float t3 = __fmul_rn(__fmul_rn(E.dfloat, rz), cz);
         raw = __fadd_rn(raw, __fadd_rn(__fsub_rn(t1, t2), t3));
         return __fmul_rn(raw, __fmul_rn(ra, cb));
-    }
-    default: {  // SCMP_EPI_ZP_SCALAR, sc/kernels.py:1198-1204
+    } else {                                                // SCMP_EPI_ZP_SCALAR, :1198-1204
         float raw = __fmul_rn(I, E.c);
         const float t1 = __fmul_rn(-u.zb, rs);
         const float t2 = __fmul_rn(u.za, cs);
         raw = __fadd_rn(raw, __fadd_rn(__fsub_rn(t1, t2), u.t3));
         return __fmul_rn(raw, u.s);
     }
+}
+
+__device__ __forceinline__ float epilogue_apply(const scmp_epilogue &E, float I, float ra,
+                                                float rz, float rs, float cb, float cz,
+                                                float cs, const EpiUniform &u) {
+    switch (E.kind) {
+    case SCMP_EPI_ROWCOL: return epilogue_apply_k<SCMP_EPI_ROWCOL>(E, I, ra, rz, rs, cb, cz, cs, u);
+    case SCMP_EPI_SCALAR: return epilogue_apply_k<SCMP_EPI_SCALAR>(E, I, ra, rz, rs, cb, cz, cs, u);
+    case SCMP_EPI_HEAD: return epilogue_apply_k<SCMP_EPI_HEAD>(E, I, ra, rz, rs, cb, cz, cs, u);
+    case SCMP_EPI_ZP_ROWCOL:
+        return epilogue_apply_k<SCMP_EPI_ZP_ROWCOL>(E, I, ra, rz, rs, cb, cz, cs, u);
+    default: return epilogue_apply_k<SCMP_EPI_ZP_SCALAR>(E, I, ra, rz, rs, cb, cz, cs, u);
     }
 }
 

@@ -46,10 +46,9 @@ __device__ __forceinline__ v16f mfma_fp4(v4i a, v4i b, v16f c) {
 // classes, when they fit), or per-class tables read from global memory.
 enum { LUT_LDS = 0, LUT_LDS_CLASSES = 1, LUT_GLOBAL = 2 };
 
-// floats of the per-wave epilogue staging area: one 32 x 32 block, rows padded to 33
-constexpr int kStageFloats = 32 * 33;
-// floats of the per-tile epilogue factors: 3 per row and 3 per column of a 256 x 256 tile
-constexpr int kFactorFloats = 6 * 256;
+// floats of the per-tile epilogue area of a 256 x 256 tile: 3 factors per row and per
+// column, then one int64 output offset per row (two floats' worth each)
+constexpr int kFactorFloats = 6 * 256 + 2 * 256;
 
 // accelerator complex dies (XCDs) of an MI355X; workgroup i runs on XCD i mod 8
 constexpr int kXcds = 8;
@@ -85,7 +84,7 @@ __device__ __forceinline__ void interleave_unit() {
     }
 }
 
-// LDS layout of both kernels: [thermometer table | stream table(s) | epilogue staging].
+// LDS layout of both kernels: [thermometer table | stream table(s) | epilogue factors].
 template <int JPF, int LUTSRC>
 __device__ __forceinline__ int fp4_tables_bytes(const GemmP &P) {
     using G = Fp4Geom<JPF>;
@@ -266,6 +265,59 @@ __device__ __forceinline__ int64_t fp4_slot(int64_t c, int64_t t, int64_t W, int
     return 2 * c + (sched_first(c, W, nwg) / ngroups == t ? 0 : 1);
 }
 
+// Fused epilogue of a finished tile, stored straight from the accumulators. In the MFMA
+// layout lane (li, h) of block (i, c) holds row 32i + 8(r>>2) + 4h + (r&3) and column
+// 32c + li of the wave's quadrant, so for each register r the 32 lanes of a half store 32
+// consecutive values of one row. Row factors and output row offsets come from LDS (nrb:
+// the lane's tile-local row of i = r = 0), column factors once per block column (mcb, mb:
+// tile-local and global column of c = 0). Only stores reach global memory.
+template <int KIND, int BA, int BB>
+__device__ __forceinline__ void fp4_drain(const GemmP &P, const v16f (&acc)[BA][BB],
+                                          const float *s_rowf, const float *s_colf,
+                                          const int64_t *s_rowo, const EpiUniform &eu,
+                                          int nrb, int mcb, int mb, int64_t ybase) {
+    float cb[BB], cz[BB], cs[BB];
+    bool mok[BB];
+#pragma unroll
+    for (int c = 0; c < BB; ++c) {
+        const int mc = mcb + 32 * c;
+        cb[c] = s_colf[mc];
+        cz[c] = s_colf[256 + mc];
+        cs[c] = s_colf[512 + mc];
+        mok[c] = mb + 32 * c < P.M;
+    }
+    constexpr bool ZP = KIND == SCMP_EPI_ZP_ROWCOL || KIND == SCMP_EPI_ZP_SCALAR;
+    constexpr bool RA = KIND == SCMP_EPI_ROWCOL || KIND == SCMP_EPI_ZP_ROWCOL;
+#pragma unroll
+    for (int i = 0; i < BA; ++i) {
+        // the 16 rows of this block row: offsets and factors first (one LDS wait), then
+        // the stores, predicated instead of branched around
+        int64_t ro[16];
+        float ra[16], rz[16], rs[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int nr = nrb + 32 * i + 8 * (r >> 2) + (r & 3);
+            ro[r] = s_rowo[nr];
+            ra[r] = RA ? s_rowf[nr] : 0.f;
+            rz[r] = KIND == SCMP_EPI_ZP_ROWCOL ? s_rowf[256 + nr] : 0.f;
+            rs[r] = ZP ? s_rowf[512 + nr] : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t o = ybase + ro[r] + mb;
+#pragma unroll
+            for (int c = 0; c < BB; ++c) {
+                if (ro[r] < 0 || !mok[c]) continue;          // row past N, column past M
+                if constexpr (KIND == SCMP_EPI_INT)
+                    P.iout[o + 32 * c] = (int32_t)acc[i][c][r];
+                else
+                    P.y[o + 32 * c] = epilogue_apply_k<KIND>(P.epi, acc[i][c][r], ra[r], rz[r],
+                                                             rs[r], cb[c], cz[c], cs[c], eu);
+            }
+        }
+    }
+}
+
 template <int JPF, int BA, int BB, int WA, int WB, int LUTSRC, bool SCHED>
 __global__ void __launch_bounds__(64 * WA * WB)
 sc_gemm_fp4_kernel(GemmP P) {
@@ -277,17 +329,19 @@ sc_gemm_fp4_kernel(GemmP P) {
     const int tabs = fp4_tables_bytes<JPF, LUTSRC>(P);
     uint8_t *sA = smem;                                  // thermometer table
     uint8_t *sB = smem + Fp4Geom<JPF>::TAB;              // stream table(s)
-    float *stg_all = (float *)(smem + ((tabs + 15) & ~15));
     constexpr int TR = WA * BA * 32, TC = WB * BB * 32;   // tile rows / columns
     static_assert(TR <= 256 && TC <= 256, "epilogue factor area holds 256 rows / columns");
-    float *s_rowf = stg_all + NW * kStageFloats;         // [3][256] sa, za, suma
+    float *s_rowf = (float *)(smem + ((tabs + 15) & ~15)); // [3][256] sa, za, suma
     float *s_colf = s_rowf + 3 * 256;                    // [3][256] sb, zb, sumb
+    int64_t *s_rowo = (int64_t *)(s_colf + 3 * 256);     // [256] output row offsets
 
     fp4_load_tables<JPF, LUTSRC, NT>(P, sA, sB);
     __syncthreads();
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    // wave index as a scalar: every per-wave offset (partial-sum blocks, staging area,
+    // operand rows) then lives in scalar registers instead of one vector register each
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5, li = lane & 31;
     const int wa = wave % WA, wb = wave / WA;
     const int ngroups = (P.D + 7) / 8;
@@ -300,8 +354,6 @@ sc_gemm_fp4_kernel(GemmP P) {
                                ? (blockIdx.x % kXcds) * (nwg / kXcds) + blockIdx.x / kXcds
                                : (int64_t)blockIdx.x;
     const int64_t u_end = sched_first(c_self + 1, W, nwg);
-    float *stg = stg_all + wave * kStageFloats;
-    const int ecol = lane & 31, ehalf = lane >> 5;
 
     for (int64_t u = sched_first(c_self, W, nwg); u < u_end;) {
         const int64_t t = u / ngroups;
@@ -330,10 +382,16 @@ sc_gemm_fp4_kernel(GemmP P) {
         fp4_accumulate<JPF, BA, BB, LUTSRC, SCHED>(P, sA, sB, pa, pb, g0, g1, h, acc,
                                                     [](int, int) {});
 
+        // The lane index, re-read inside the tile loop through an opaque copy: offsets
+        // derived from it are then computed here, when needed, instead of being hoisted
+        // out of the loop into registers that the main loop's pressure would spill.
+        int lt = lane;
+        asm volatile("" : "+v"(lt));
+        const int ecol = lt & 31, ehalf = lt >> 5;
         // partial-sum slot layout: block (i, c) of this wave, then lane, then the 16
         // accumulator registers of the lane (the MFMA layout itself, 64 B per lane)
         auto pblk = [&](int i, int c) __attribute__((always_inline)) {
-            return (int64_t)((wave * BA + i) * BB + c) * 1024 + lane * 16;
+            return (int64_t)((wave * BA + i) * BB + c) * 1024 + lt * 16;
         };
 
         const bool shared = g0 != 0 || g1 != ngroups;
@@ -408,6 +466,10 @@ sc_gemm_fp4_kernel(GemmP P) {
             const int tr0 = ta * TR, tc0 = tb * TC;
             const bool fp32 = P.epi.kind != SCMP_EPI_INT;
             __syncthreads();          // every wave is past the previous tile's last store
+            // where each row of the tile goes (row map applied, times ldy; -1 past N): the
+            // drain below then issues no loads, so no store ever waits for another
+            for (int e = tid; e < TR; e += NT)
+                s_rowo[e] = tr0 + e < P.N ? out_row(P.row_map, tr0 + e) * P.ldy : (int64_t)-1;
             if (fp32) {
                 for (int e = tid; e < TR; e += NT) {
                     float f[3] = {0.f, 0.f, 0.f};
@@ -426,38 +488,32 @@ sc_gemm_fp4_kernel(GemmP P) {
             }
             const EpiUniform eu = fp32 ? epi_uniform(P.epi, batch) : EpiUniform{0.f, 0.f, 0.f, 0.f};
             __syncthreads();
-            // fused epilogue: every block leaves the accumulators through this wave's LDS
-            // staging area (written in the MFMA layout, read back row-wise: lanes 0-31 /
-            // 32-63 take 32 consecutive m of rows 2k / 2k+1) and is stored with its fp32
-            // epilogue. Only stores reach global memory here.
-            float *__restrict__ yout = P.y;
-            int32_t *__restrict__ iout = P.iout;
+            const int nrb = wa * (BA * 32) + 4 * ehalf;
+            const int mcb = wb * (BB * 32) + ecol;
+            const int mb = tc0 + mcb;
             const int64_t ybase = batch * P.bsy;
-#pragma unroll
-            for (int i = 0; i < BA; ++i)
-#pragma unroll
-                for (int c = 0; c < BB; ++c) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        stg[(8 * (r >> 2) + 4 * h + (r & 3)) * 33 + li] = acc[i][c][r];
-                    __syncthreads();
-                    const int m = b0 + 32 * c + ecol, mc = m - tc0;
-#pragma unroll 4
-                    for (int rr = ehalf; rr < 32; rr += 2) {
-                        const float v = stg[rr * 33 + ecol];
-                        const int n = a0 + 32 * i + rr, nr = n - tr0;
-                        if (n < P.N && m < P.M) {
-                            const int64_t o = ybase + out_row(P.row_map, n) * P.ldy + m;
-                            if (!fp32)
-                                iout[o] = (int32_t)v;
-                            else
-                                yout[o] = epilogue_apply(P.epi, v, s_rowf[nr], s_rowf[256 + nr],
-                                                         s_rowf[512 + nr], s_colf[mc],
-                                                         s_colf[256 + mc], s_colf[512 + mc], eu);
-                        }
-                    }
-                    __syncthreads();
-                }
+            switch (P.epi.kind) {
+            case SCMP_EPI_INT:
+                fp4_drain<SCMP_EPI_INT>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                break;
+            case SCMP_EPI_ROWCOL:
+                fp4_drain<SCMP_EPI_ROWCOL>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                break;
+            case SCMP_EPI_SCALAR:
+                fp4_drain<SCMP_EPI_SCALAR>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                break;
+            case SCMP_EPI_HEAD:
+                fp4_drain<SCMP_EPI_HEAD>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                break;
+            case SCMP_EPI_ZP_ROWCOL:
+                fp4_drain<SCMP_EPI_ZP_ROWCOL>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb,
+                                              ybase);
+                break;
+            default:
+                fp4_drain<SCMP_EPI_ZP_SCALAR>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb,
+                                              ybase);
+                break;
+            }
         }
         u = t * ngroups + g1;
     }
@@ -533,18 +589,34 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
     };
     fp4_accumulate<JPF, BA, BB, LUTSRC, false>(P, sA, sB, pa, pb, 0, ngroups, h, acc, after);
 
+    // two store loops so that the common one (no row map) issues no loads between stores
+    float *__restrict__ ybat = P.y + batch * P.bsy;
+    if (P.row_map == nullptr) {
 #pragma unroll
-    for (int c = 0; c < BB; ++c) {
-        const int m = b0 + 32 * c + li;
-        if (m >= P.M) continue;
+        for (int c = 0; c < BB; ++c) {
+            const int m = b0 + 32 * c + li;
+            if (m >= P.M) continue;
 #pragma unroll
-        for (int i = 0; i < BA; ++i)
+            for (int i = 0; i < BA; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (n >= P.N) continue;
-                P.y[batch * P.bsy + out_row(P.row_map, n) * P.ldy + m] = yac[i][c][r];
-            }
+                for (int r = 0; r < 16; ++r) {
+                    const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (n < P.N) ybat[(int64_t)n * P.ldy + m] = yac[i][c][r];
+                }
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < BB; ++c) {
+            const int m = b0 + 32 * c + li;
+            if (m >= P.M) continue;
+#pragma unroll
+            for (int i = 0; i < BA; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (n < P.N) ybat[P.row_map[n] * P.ldy + m] = yac[i][c][r];
+                }
+        }
     }
 }
 
@@ -579,7 +651,7 @@ static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
     GemmP P = P0;
     auto kern = sc_gemm_fp4_kernel<JPF, BA, BB, WA, WB, LUTSRC, true>;
     const size_t lds = ((fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15) +
-                       ((size_t)WA * WB * kStageFloats + kFactorFloats) * sizeof(float);
+                       (size_t)kFactorFloats * sizeof(float);
     int rc = fp4_set_lds(kern, lds);
     if (rc != SCMP_OK) return rc;
     kern<<<dim3((unsigned)P.nwg), 64 * WA * WB, lds, stream>>>(P);
@@ -609,7 +681,7 @@ static int launch_fp4_chunked(const GemmP &P0, int64_t batch, hipStream_t stream
 template <int JPF>
 int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t s) {
     using G = Fp4Geom<JPF>;
-    const int64_t stage = (4 * kStageFloats + kFactorFloats) * (int64_t)sizeof(float);
+    const int64_t stage = kFactorFloats * (int64_t)sizeof(float);
     if (P.d_class == nullptr)
         return chunked ? launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s)
                        : launch_fp4_main<JPF, LUT_LDS>(P, batch, s);

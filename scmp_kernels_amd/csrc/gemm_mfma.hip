@@ -342,25 +342,33 @@ sc_gemm_mfma_kernel(GemmP P) {
     // Non-chunked kernels store the exact int32 I; the fp32 epilogue runs as a separate
     // elementwise pass (epilogue_kernel, in place over the same buffer). Fusing it here
     // makes the register allocator move all accumulators out of the AGPRs and spill.
+    // One loop per row mapping, so that the common one (no row map) issues no loads
+    // between its stores (a load's wait would also wait for every store before it).
+    auto store_all = [&](auto row_of) __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < BB; ++c) {
-        const int m = b0 + 32 * c + li;
-        if (m >= P.M) continue;
+        for (int c = 0; c < BB; ++c) {
+            const int m = b0 + 32 * c + li;
+            if (m >= P.M) continue;
 #pragma unroll
-        for (int i = 0; i < BA; ++i) {
+            for (int i = 0; i < BA; ++i) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (n >= P.N) continue;
-                const int64_t o = batch * P.bsy + out_row(P.row_map, n) * P.ldy + m;
-                if (CHUNKED) {
-                    P.y[o] = yac[CHUNKED ? i : 0][CHUNKED ? c : 0][r];
-                    continue;
+                for (int r = 0; r < 16; ++r) {
+                    const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (n >= P.N) continue;
+                    const int64_t o = batch * P.bsy + row_of(n) * P.ldy + m;
+                    if (CHUNKED) {
+                        P.y[o] = yac[CHUNKED ? i : 0][CHUNKED ? c : 0][r];
+                        continue;
+                    }
+                    P.iout[o] = acc[i][c][r];
                 }
-                P.iout[o] = acc[i][c][r];
             }
         }
-    }
+    };
+    if (P.row_map == nullptr)
+        store_all([](int n) { return (int64_t)n; });
+    else
+        store_all([&](int n) { return P.row_map[n]; });
 }
 
 // fp32 epilogues of the reference paths, applied to the int32 accumulator in place

@@ -85,11 +85,12 @@ sc_gemm_valu_kernel(const uint8_t *ca, int64_t lda, int64_t bsa, const uint8_t *
     for (int i = 0; i < 4; ++i) {
         const int n = a0 + 4 * ty + i;
         if (n >= N) continue;
+        const int64_t row = out_row(row_map, n);     // one row-map load per row
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int m = b0 + 4 * tx + c;
             if (m >= M) continue;
-            const int64_t o = batch * bsy + out_row(row_map, n) * ldy + m;
+            const int64_t o = batch * bsy + row * ldy + m;
             const int I = acc[i][c];
             if (E.kind == SCMP_EPI_INT) iout[o] = I;
             else y[o] = epilogue_value(E, (float)I, n, m, batch);
