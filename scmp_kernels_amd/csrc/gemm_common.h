@@ -29,9 +29,11 @@ struct GemmP {
     int64_t ldy, bsy;
     int tilesA, tilesB;
     int nclass;
-    // persistent FP4 schedule: ntiles = tilesA * tilesB * batch tiles of 256 x 256, nwg
-    // workgroups; split tiles keep exact partial sums in part (2 slots of 256 x 256 floats
-    // per workgroup) and count contributors in cnt (ntiles ints, zero on entry)
+    // persistent FP4 schedule: ntiles = tilesA * tilesB * batch tiles of 256 x tile_cols
+    // (256, or 64 for narrow outputs), nwg workgroups; split tiles keep exact partial sums
+    // in part (2 slots of one tile's floats per workgroup) and count contributors in cnt
+    // (ntiles ints, zero on entry)
+    int tile_cols;
     int64_t ntiles;
     int nwg;
     float *part;

@@ -19,9 +19,10 @@ static int device_cu_count() {
     return cached[dev];
 }
 
-// Schedule of the non-chunked FP4 kernel (256 x 256 tiles, one workgroup per CU).
+// Schedule of the non-chunked FP4 kernel (256 x TC tiles, one workgroup per CU).
 struct Fp4Plan {
     int64_t tilesA, tilesB, ntiles;
+    int TC;                   // tile columns: 256, or 64 when M <= 64 (narrow tiles)
     int nwg;                  // persistent workgroups
     bool split;               // some tiles are shared by several workgroups
     int64_t cnt_bytes, part_bytes;
@@ -29,11 +30,15 @@ struct Fp4Plan {
 
 // Each workgroup takes an equal share of the (tile, 8-d group) work list. Tiles are shared
 // only when it pays: inner dimension of at least 64 groups (512 d), and at least 32 groups
-// per workgroup. Otherwise every workgroup takes whole tiles.
-static Fp4Plan fp4_plan(int64_t N, int64_t M, int64_t D, int64_t batch, int ncu) {
+// per workgroup. Otherwise every workgroup takes whole tiles. Outputs at most 64 columns
+// wide (attention's P.V per head) use 256 x 64 tiles when the stream table is a single one
+// (narrow_ok), instead of computing three quarters of a 256 x 256 tile on padding.
+static Fp4Plan fp4_plan(int64_t N, int64_t M, int64_t D, int64_t batch, int ncu,
+                        bool narrow_ok) {
     Fp4Plan p;
+    p.TC = narrow_ok && M <= 64 ? 64 : 256;
     p.tilesA = cdiv(N, 256);
-    p.tilesB = cdiv(M, 256);
+    p.tilesB = cdiv(M, p.TC);
     p.ntiles = p.tilesA * p.tilesB * batch;
     const int64_t G = cdiv(D, 8);
     const int64_t W = p.ntiles * G;
@@ -50,7 +55,7 @@ static Fp4Plan fp4_plan(int64_t N, int64_t M, int64_t D, int64_t batch, int ncu)
     p.nwg = (int)nwg;
     p.split = (W % p.nwg) != 0 || (W / p.nwg) % G != 0;
     p.cnt_bytes = (p.ntiles * 4 + 255) / 256 * 256;
-    p.part_bytes = (int64_t)p.nwg * 2 * 65536 * 4;
+    p.part_bytes = (int64_t)p.nwg * 2 * (256 * p.TC) * 4;
     return p;
 }
 
@@ -58,6 +63,9 @@ __global__ void zero_ints_kernel(int *p, int64_t n) {
     const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0;
 }
+
+// Narrow tiles are instantiated for a single stream table in LDS (no per-d classes).
+static bool fp4_narrow_ok(const scmp_gemm_args &a) { return a.d_class == nullptr; }
 
 static int fp4_launch_jpf(const GemmP &P, int64_t batch, int JPF, bool chunked,
                           hipStream_t stream) {
@@ -73,7 +81,8 @@ static int fp4_launch_jpf(const GemmP &P, int64_t batch, int JPF, bool chunked,
 int gemm_fp4_run(GemmP &P, const scmp_gemm_args &a, bool chunked, hipStream_t stream) {
     const int JPF = a.JP < 32 ? 32 : a.JP;
     if (chunked) return fp4_launch_jpf(P, a.batch, JPF, true, stream);
-    Fp4Plan plan = fp4_plan(a.N, a.M, a.D, a.batch, device_cu_count());
+    Fp4Plan plan = fp4_plan(a.N, a.M, a.D, a.batch, device_cu_count(), fp4_narrow_ok(a));
+    P.tile_cols = plan.TC;
     P.tilesA = (int)plan.tilesA;
     P.tilesB = (int)plan.tilesB;
     P.ntiles = plan.ntiles;
@@ -134,7 +143,7 @@ extern "C" int64_t scmp_sc_gemm_workspace_bytes(const scmp_gemm_args *a) {
     if (!a || a->impl != SCMP_GEMM_MFMA_FP4 || a->N <= 0 || a->M <= 0 || a->D <= 0 ||
         a->batch <= 0 || (a->chunk > 0 && a->chunk < a->D))
         return 0;
-    const Fp4Plan p = fp4_plan(a->N, a->M, a->D, a->batch, device_cu_count());
+    const Fp4Plan p = fp4_plan(a->N, a->M, a->D, a->batch, device_cu_count(), fp4_narrow_ok(*a));
     return p.split ? p.cnt_bytes + p.part_bytes : 0;
 }
 

@@ -642,12 +642,14 @@ static size_t fp4_tables_bytes_host(const GemmP &P) {
     return (size_t)G::TAB * (1 + (LUTSRC == LUT_LDS ? 1 : LUTSRC == LUT_LDS_CLASSES ? P.nclass : 0));
 }
 
-// Non-chunked: 256 x 256 tiles, each wave 128 x 128 (4 x 4 blocks of 32 x 32), MFMA /
-// LDS-read interleaving enforced, epilogue fused; P.nwg persistent workgroups (P.ntiles
-// when no split workspace was given: one tile each, no partial sums).
-template <int JPF, int LUTSRC>
+// Non-chunked: 256 x 256 tiles, each wave 128 x 128 (4 x 4 blocks of 32 x 32), or narrow
+// 256 x 64 tiles, each wave 64 x 64 (2 x 2 blocks); MFMA / LDS-read interleaving enforced,
+// epilogue fused; P.nwg persistent workgroups (P.ntiles when no split workspace was given:
+// one tile each, no partial sums).
+template <int JPF, int LUTSRC, bool NARROW = false>
 static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
-    constexpr int BA = 4, BB = 4, WA = 2, WB = 2;
+    constexpr int BA = NARROW ? 2 : 4, BB = NARROW ? 2 : 4, WA = NARROW ? 4 : 2,
+                  WB = NARROW ? 1 : 2;
     GemmP P = P0;
     auto kern = sc_gemm_fp4_kernel<JPF, BA, BB, WA, WB, LUTSRC, true>;
     const size_t lds = ((fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15) +
@@ -682,9 +684,11 @@ template <int JPF>
 int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t s) {
     using G = Fp4Geom<JPF>;
     const int64_t stage = kFactorFloats * (int64_t)sizeof(float);
-    if (P.d_class == nullptr)
-        return chunked ? launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s)
-                       : launch_fp4_main<JPF, LUT_LDS>(P, batch, s);
+    if (P.d_class == nullptr) {
+        if (chunked) return launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s);
+        return P.tile_cols == 64 ? launch_fp4_main<JPF, LUT_LDS, true>(P, batch, s)
+                                 : launch_fp4_main<JPF, LUT_LDS>(P, batch, s);
+    }
     if (P.nclass > 0 && (int64_t)G::TAB * (1 + P.nclass) + stage <= kFp4MaxLds)
         return chunked ? launch_fp4_chunked<JPF, LUT_LDS_CLASSES>(P, batch, s)
                        : launch_fp4_main<JPF, LUT_LDS_CLASSES>(P, batch, s);

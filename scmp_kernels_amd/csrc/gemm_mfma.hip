@@ -486,6 +486,7 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     P.epi = a.epi; P.y = a.y; P.ldy = a.ldy; P.bsy = a.bsy;
     P.row_map = a.row_map;
     P.tilesA = 0;
+    P.tile_cols = 256;
     P.nclass = a.nclass;
     if (a.impl == SCMP_GEMM_MFMA_FP4) {
         // the FP4 kernel applies the epilogue itself (int32 I for SCMP_EPI_INT)

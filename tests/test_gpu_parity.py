@@ -383,6 +383,10 @@ RANDOM_CASES = [
     ("per_row", dict(mode="bipolar", halve_bipolar_stoc_len=True), (64, 64, 128)),
     ("per_tensor", dict(mode="bipolar"), (32, 64, 256)),
     ("per_tensor", dict(mode="unipolar"), (40, 33, 100)),
+    # outputs at most 64 wide: 256 x 64 tiles, shared between workgroups (split partial
+    # sums) at these inner dimensions
+    ("per_row", dict(mode="bipolar"), (1000, 64, 1024)),
+    ("per_row", dict(mode="bipolar"), (700, 40, 2048)),
 ]
 
 
