@@ -136,7 +136,8 @@ typedef struct scmp_quant_args {
     float host_inv, host_zp;  /* HOST_* variants: reciprocal scale and zero-point */
     /* GEMM codes: the input rows form batches of code_batch_rows rows (0: one batch);
      * batch b, row i goes to code[(b * code_rows + i) * code_ld + col]; rows
-     * code_batch_rows..code_rows-1 of every batch and columns cols..code_ld-1 are zero */
+     * code_batch_rows..code_rows-1 of every batch and columns cols..code_ld-1 are zero;
+     * code_ld >= cols rounded up to a multiple of 4 */
     int code_kind;
     uint8_t *code;
     int64_t code_ld, code_rows, code_batch_rows;

@@ -332,6 +332,32 @@ __device__ __forceinline__ void load_chunk4(const scmp_quant_args &a, int64_t r,
     }
 }
 
+// Workgroup w of nw zeroes its share of the padding rows [cbr, code_rows) of every batch of
+// the code buffer (16-byte stores when the rows allow them), so no separate launch is needed.
+__device__ __forceinline__ void zero_pad_share(const scmp_quant_args &a, int64_t cbr, int64_t w,
+                                               int64_t nw) {
+    const int64_t pad_rows = a.code_rows - cbr;
+    if (pad_rows <= 0) return;
+    const int64_t nb = a.rows / cbr;
+    const bool wide = (a.code_ld & 15) == 0 && ((uintptr_t)a.code & 15) == 0;
+    const int64_t ub = wide ? 16 : 1;                      // bytes per unit
+    const int64_t per = pad_rows * a.code_ld / ub;         // units per batch
+    const int64_t total = per * nb;
+    const int64_t u0 = total * w / nw, u1 = total * (w + 1) / nw;
+    int64_t b = (u0 + threadIdx.x) / per;
+    int64_t off = (u0 + threadIdx.x) - b * per;
+    for (int64_t u = u0 + threadIdx.x; u < u1; u += kGroupThreads) {
+        uint8_t *dst = a.code + (b * a.code_rows + cbr) * a.code_ld + off * ub;
+        if (wide) *(uint4 *)dst = make_uint4(0u, 0u, 0u, 0u);
+        else *dst = 0;
+        off += kGroupThreads;
+        while (off >= per) {
+            off -= per;
+            ++b;
+        }
+    }
+}
+
 // PT: register-held chunks per thread (npt <= PT); npt > PT re-reads the chunks instead.
 template <int OP, int SM, int PT>
 __global__ void __launch_bounds__(kGroupThreads)
@@ -351,15 +377,19 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         for (int i = tid; i < nr; i += kGroupThreads) rsums[i] = 0.0f;
     if (lds_jtab) s_jtab[tid] = a.jtab[tid];
 
-    // position (row, first column) of this thread's k-th chunk, chunk index tid + 256 k
+    // position (row, first column) of this thread's k-th chunk, chunk index tid + 256 k;
+    // a step of 256 chunks is dr rows and dc chunks
     const int rr_first = tid / cpr;
     const int cc_first = tid - rr_first * cpr;
+    const int dr = kGroupThreads / cpr, dc = kGroupThreads - dr * cpr;
+    auto step_rows = [&](int &cc) __attribute__((always_inline)) {
+        cc += dc;
+        const bool wrap = cc >= cpr;
+        if (wrap) cc -= cpr;
+        return dr + (wrap ? 1 : 0);
+    };
     auto advance = [&](int &rr, int &cc) __attribute__((always_inline)) {
-        cc += kGroupThreads;
-        while (cc >= cpr) {
-            cc -= cpr;
-            ++rr;
-        }
+        rr += step_rows(cc);
     };
 
     // pass 1: statistic of the group
@@ -477,11 +507,14 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
                 }
             }
         }
+        // columns past the row end (the last chunk of a row whose length is not a multiple
+        // of 4) get code 0 and add nothing to the row sum
+        const int nv = a.cols - c;
         uint32_t word = 0;
         float qs = 0.0f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const float q = fmin_first(fmax_first(t[k], qlo), qf);
+            const float q = k < nv ? fmin_first(fmax_first(t[k], qlo), qf) : 0.0f;
             const int qi = (int)q;
             uint32_t code;
             if (thermo) {
@@ -490,33 +523,43 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
             } else {
                 code = (uint32_t)(qi & 0xff);
             }
-            word |= code << (8 * k);
+            word |= (k < nv ? code : 0u) << (8 * k);
             qs += q;
         }
         *(uint32_t *)(crow + c) = word;
         if (want_sum) atomicAdd(&rsums[rr], qs);
     };
-    const bool fast = full && !api_out && a.code && !(thermo && !lds_jtab);
-    if (reg && fast) {
+    const bool fast = !api_out && a.code && !(thermo && !lds_jtab);
+    if (fast) {
         // code row of input row r0 + rr: batch bb, row bi of the batch; tracked as rr grows
+        // (a step that leaves a batch skips that batch's padding rows)
         const int64_t rf0 = r0 + rr_first;
         int64_t bb = rf0 / cbr, bi = rf0 - bb * cbr;
         uint8_t *crow = a.code + (bb * a.code_rows + bi) * a.code_ld;
         int rr = rr_first, cc = cc_first;
+        auto advance_code = [&]() __attribute__((always_inline)) {
+            const int n = step_rows(cc);
+            rr += n;
+            bi += n;
+            crow += (int64_t)n * a.code_ld;
+            while (bi >= cbr) {
+                bi -= cbr;
+                crow += (a.code_rows - cbr) * a.code_ld;
+            }
+        };
+        if (reg) {
 #pragma unroll
-        for (int k = 0; k < PT; ++k) {
-            if (k < npt && tid + k * kGroupThreads < nch) emit_fast(vals[k], rr, crow, 4 * cc);
-            cc += kGroupThreads;
-            while (cc >= cpr) {
-                cc -= cpr;
-                ++rr;
-                if (++bi == cbr) {
-                    bi = 0;
-                    ++bb;
-                    crow = a.code + bb * a.code_rows * a.code_ld;
-                } else {
-                    crow += a.code_ld;
-                }
+            for (int k = 0; k < PT; ++k) {
+                if (k < npt && tid + k * kGroupThreads < nch)
+                    emit_fast(vals[k], rr, crow, 4 * cc);
+                advance_code();
+            }
+        } else {
+            for (int ch = tid; ch < nch; ch += kGroupThreads) {
+                float v[4];
+                load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, v);
+                emit_fast(v, rr, crow, 4 * cc);
+                advance_code();
             }
         }
     } else if (reg) {
@@ -545,6 +588,7 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
             a.code[(b * a.code_rows + i) * a.code_ld + c] = 0;
         }
     }
+    if (a.code) zero_pad_share(a, cbr, blockIdx.x, gridDim.x);
     __syncthreads();
     for (int rr = tid; rr < nr; rr += kGroupThreads) {
         const int64_t r = r0 + rr;
@@ -797,18 +841,7 @@ static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stre
         launch_group<QOP_MUL>(a, grid, (int)G, (int)cpr, npt, vec, stream);
         break;
     }
-    SCMP_LAUNCH_CHECK("scmp_quantize/group");
-    if (a.code) {
-        const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
-        if (a.code_rows > cbr) {
-            const int64_t total = (a.code_rows - cbr) * a.code_ld * (a.rows / cbr);
-            int64_t blocks = cdiv(total, 256);
-            if (blocks > 4096) blocks = 4096;
-            zero_code_rows_kernel<<<blocks, 256, 0, stream>>>(a.code, a.code_ld, a.code_rows,
-                                                              cbr, a.rows / cbr);
-            SCMP_LAUNCH_CHECK("scmp_quantize/pad");
-        }
-    }
+    SCMP_LAUNCH_CHECK("scmp_quantize/group");   // the kernel zeroes the padding rows too
     return SCMP_OK;
 }
 
@@ -844,8 +877,10 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
         const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
         SCMP_REQUIRE(a.rows % cbr == 0, "scmp_quantize: rows %lld not a multiple of the "
                      "batch rows %lld", (long long)a.rows, (long long)cbr);
-        SCMP_REQUIRE(a.code_ld >= a.cols && a.code_rows >= cbr,
-                     "scmp_quantize: code buffer rows/ld (%lld, %lld) smaller than the input",
+        // codes are written as 4-byte words per 4-column chunk
+        SCMP_REQUIRE(a.code_ld >= 4 * cdiv(a.cols, 4) && a.code_rows >= cbr,
+                     "scmp_quantize: code buffer rows/ld (%lld, %lld) smaller than the input "
+                     "(ld must cover cols rounded up to 4)",
                      (long long)a.code_rows, (long long)a.code_ld);
         SCMP_REQUIRE(a.code_kind == SCMP_CODE_Q || (a.code_kind == SCMP_CODE_THERMO && a.jtab),
                      "scmp_quantize: THERMO codes need jtab");

@@ -258,6 +258,40 @@ def test_quant_codes_near_half_integers(asym, smooth_mode):
     assert not got[rows:].any()                  # padding rows are zero
 
 
+@pytest.mark.parametrize("asym", [False, True])
+@pytest.mark.parametrize("cols,rows,G,cbr", [(197, 39, 5, 13), (198, 39, 5, 13),
+                                             (199, 39, 13, 13), (197, 200, 100, 200)])
+def test_quant_codes_ragged_columns_and_padding(asym, cols, rows, G, cbr):
+    """Row-group quantizer codes when the row length is not a multiple of 4 (the last
+    4-column chunk is partial), in batches of cbr rows, with the padding rows of every batch
+    and the columns past the row end pre-filled with garbage: codes equal the oracle's,
+    padding is zero, row sums count only real columns. The (197, 200, 100) case holds more
+    chunks per group than the registers do (the re-reading path)."""
+    from scmp_kernels_amd import _lib
+    from scmp_kernels_amd.sc import kernels as K
+    Q = 255 if asym else 127
+    x = np.random.default_rng(cols + rows + G).standard_normal((rows, cols)).astype(np.float32)
+    if asym:
+        _, _, ref_q = O.grouped_asym(x, G, Q)
+    else:
+        _, ref_q, _ = O.grouped_sym(x, G, Q)
+    ref = (ref_q.astype(np.int32) & 0xff).astype(np.uint8)
+    nb = rows // cbr
+    ld = (cols + 15) // 16 * 16
+    code = torch.full((nb, cbr + 19, ld), 0x5A, dtype=torch.uint8, device=_dev())
+    rs = torch.full((rows,), -1.0, dtype=torch.float32, device=_dev()) if asym else None
+    ws = K.quantize(T(x), _lib.Q_GROUP_ASYM if asym else _lib.Q_GROUP_SYM, Q, 256, group=G,
+                    code=code, code_kind=_lib.CODE_Q, code_batch_rows=cbr, rowsum=rs)
+    got = code.cpu().numpy()
+    del ws
+    np.testing.assert_array_equal(got[:, :cbr, :cols].reshape(rows, cols), ref)
+    assert not got[:, :cbr, cols:].any()          # columns past the row end
+    assert not got[:, cbr:, :].any()              # padding rows of every batch
+    if asym:
+        np.testing.assert_array_equal(rs.cpu().numpy(),
+                                      ref_q.astype(np.float64).sum(axis=1).astype(np.float32))
+
+
 # -------------------------------------------------------------------------------------
 # the SC GEMM: integer accumulator against the oracle
 # -------------------------------------------------------------------------------------
