@@ -519,26 +519,44 @@ sc_gemm_fp4_kernel(GemmP P) {
     }
 }
 
-template <int JPF, int BA, int BB, int WA, int WB, int LUTSRC>
+template <int JPF, int BA, int BB, int WA, int WB, int LUTSRC, bool SLDS>
 __global__ void __launch_bounds__(64 * WA * WB)
 sc_gemm_fp4_chunked_kernel(GemmP P) {
     constexpr int NT = 64 * WA * WB;
+    constexpr int TR = WA * BA * 32, TC = WB * BB * 32;   // tile rows / columns
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t *sA = smem;
     uint8_t *sB = smem + Fp4Geom<JPF>::TAB;
+    const int tid = threadIdx.x;
+    const int ta = blockIdx.x % P.tilesA, tb = blockIdx.x / P.tilesA;
+    const int batch = blockIdx.z;
+    const int D = P.D;
+    const int ngroups = (D + 7) / 8;
+    const int nchunks = (D + P.chunk - 1) / P.chunk;
+    // SLDS: every chunk's scales of the tile's rows and columns sit in LDS
+    // ([chunk][TR] then [chunk][TC], zero past N / M), so the chunk epilogue in the main
+    // loop issues no global load (whose wait would also wait for the code loads in flight)
+    float *s_sa = (float *)(smem + ((fp4_tables_bytes<JPF, LUTSRC>(P) + 15) & ~15));
+    float *s_sb = s_sa + nchunks * TR;
     fp4_load_tables<JPF, LUTSRC, NT>(P, sA, sB);
+    if (SLDS) {
+        const int tr0 = ta * TR, tc0 = tb * TC;
+        for (int e = tid; e < nchunks * TR; e += NT) {
+            const int k = e / TR, r = e - k * TR;
+            s_sa[e] = tr0 + r < P.N ? P.epi.sa[(int64_t)k * P.epi.sa_chunk_stride + tr0 + r] : 0.f;
+        }
+        for (int e = tid; e < nchunks * TC; e += NT) {
+            const int k = e / TC, c = e - k * TC;
+            s_sb[e] = tc0 + c < P.M ? P.epi.sb[(int64_t)k * P.epi.sb_chunk_stride + tc0 + c] : 0.f;
+        }
+    }
     __syncthreads();
 
-    const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, li = lane & 31;
     const int wa = wave % WA, wb = wave / WA;
-    const int ta = blockIdx.x % P.tilesA, tb = blockIdx.x / P.tilesA;
-    const int batch = blockIdx.z;
     const int a0 = (ta * WA + wa) * (BA * 32);
     const int b0 = (tb * WB + wb) * (BB * 32);
-    const int D = P.D;
-    const int ngroups = (D + 7) / 8;
 
     const uint8_t *pa[BA];
     const uint8_t *pb[BB];
@@ -569,16 +587,18 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
         const float cc = P.epi.c;
         const float *sa = P.epi.sa + (int64_t)kchunk * P.epi.sa_chunk_stride;
         const float *sb = P.epi.sb + (int64_t)kchunk * P.epi.sb_chunk_stride;
+        const int lsa0 = (kchunk - ta) * TR;                 // s_sa[lsa0 + n]: row n
+        const int lsb0 = (kchunk - tb) * TC;                 // s_sb[lsb0 + m]: column m
 #pragma unroll
         for (int c = 0; c < BB; ++c) {
             const int m = b0 + 32 * c + li;
-            const float sbm = m < P.M ? sb[m] : 0.0f;
+            const float sbm = SLDS ? s_sb[lsb0 + m] : (m < P.M ? sb[m] : 0.0f);
 #pragma unroll
             for (int i = 0; i < BA; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int n = a0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                    const float san = n < P.N ? sa[n] : 0.0f;
+                    const float san = SLDS ? s_sa[lsa0 + n] : (n < P.N ? sa[n] : 0.0f);
                     const float raw = __fmul_rn(acc[i][c][r], cc);
                     const float term = __fmul_rn(raw, __fmul_rn(san, sbm));
                     yac[i][c][r] = __fadd_rn(yac[i][c][r], term);
@@ -668,8 +688,12 @@ static int launch_fp4_chunked(const GemmP &P0, int64_t batch, hipStream_t stream
     GemmP P = P0;
     P.tilesA = (int)cdiv(P.N, WA * BA * 32);
     const int64_t tilesB = cdiv(P.M, WB * BB * 32);
-    auto kern = sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC>;
-    const size_t lds = fp4_tables_bytes_host<JPF, LUTSRC>(P);
+    const size_t tabs = (fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15;
+    const size_t scales = (size_t)cdiv(P.D, P.chunk) * (WA * BA * 32 + WB * BB * 32) * sizeof(float);
+    const bool slds = tabs + scales <= (size_t)kFp4MaxLds;
+    auto kern = slds ? sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC, true>
+                     : sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC, false>;
+    const size_t lds = slds ? tabs + scales : tabs;
     int rc = fp4_set_lds(kern, lds);
     if (rc != SCMP_OK) return rc;
     kern<<<dim3((unsigned)(P.tilesA * tilesB), 1, (unsigned)batch), 64 * WA * WB, lds,
