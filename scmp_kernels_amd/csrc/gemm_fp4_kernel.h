@@ -120,18 +120,24 @@ __device__ __forceinline__ void fp4_load_tables(const GemmP &P, uint8_t *sA, uin
 }
 
 // acc += the products of inner-dimension groups [g0, g1) (8 d per group) for the operand
-// rows at pa[i] (A, BA blocks of 32) and pb[c] (B, BB blocks of 32). Each pipeline unit
+// rows of the wave's A blocks (BA blocks of 32 rows from the wave-uniform address abase,
+// row stride lda) and B blocks (BB from bbase, stride ldb); the lane's row li of each block
+// is addressed by a 32-bit offset from that scalar base. Each pipeline unit
 // (up to two k-steps of one d, or two d for JPF = 32) is loaded one unit ahead into the
 // other of two fragment sets, so the LDS reads of unit u+1 overlap the MFMAs of unit u.
-// The code bytes of a group (one uint2 per operand row) live in one of two buffers that
-// alternate by group parity: the loads for group g+2 are issued into the buffer group g
-// has just finished with, a whole group before they are read, and no register ever has
-// to wait for a load issued in the same group. after(d0, d1) runs once the MFMAs of
-// inner dimensions d0..d1 are all issued.
+// Code bytes: the A side loads one uint2 per row and group into one of two buffers that
+// alternate by group parity (group g+2's codes are issued when group g ends); the B side
+// loads one 16-byte pair of groups (gp, gp+1) per row, half the load instructions and
+// cache-line requests of one load per group, and the pair after next is issued when a
+// pair ends. Either way a load is read two groups after it is issued, and no wait covers a
+// load issued in the same group. A pair load never reads past a code row: its address is
+// clamped to the row's last two groups (the pair's first group then sits in the upper
+// half, `shift` 1; only a segment's lone last group can be so). after(d0, d1) runs once
+// the MFMAs of inner dimensions d0..d1 are all issued.
 template <int JPF, int BA, int BB, int LUTSRC, bool SCHED, class After>
 __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA,
-                                               const uint8_t *sB, const uint8_t *const *pa,
-                                               const uint8_t *const *pb, int g0, int g1,
+                                               const uint8_t *sB, const uint8_t *abase,
+                                               const uint8_t *bbase, int li, int g0, int g1,
                                                int h, v16f (&acc)[BA][BB], After after) {
     using G = Fp4Geom<JPF>;
     constexpr int ROWB = G::ROWB, KSU = G::KSU, SPD = G::SPD, UPG = G::UPG, LS = G::LS,
@@ -139,34 +145,61 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     constexpr int NR = BA + BB;                  // code rows per lane: A rows, then B rows
     const uint8_t *glut = (const uint8_t *)P.lut;
     const int D = P.D;
+    const int ngroups = (D + 7) / 8;
+    const int glast = ngroups >= 2 ? ngroups - 2 : 0;   // last pair address (in groups)
 
     // With per-d table classes, lane l also loads the class of inner dimension 8g + (l & 7)
-    // of the group into cls; a unit takes its d's class from that lane (v_readlane), so the
+    // of each group into cls; a unit takes its d's class from that lane (v_readlane), so the
     // class costs no memory wait inside the loop.
     const int lane8 = (int)(threadIdx.x & 7);
-    auto load_codes = [&](uint2 (&c)[NR], int &cls, int g) __attribute__((always_inline)) {
+    // lane offsets of row li of block 0 (a block is 32 rows further); all below 2^31, as
+    // the host bounds D (and so the row strides) by 65536
+    const uint32_t lda = (uint32_t)P.lda, ldb = (uint32_t)P.ldb;
+    const uint32_t oa = (uint32_t)li * lda, ob = (uint32_t)li * ldb;
+    auto load_a = [&](uint2 (&c)[BA], int &cls, int g) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < BA; ++i) c[i] = *(const uint2 *)(pa[i] + 8 * g);
-#pragma unroll
-        for (int j = 0; j < BB; ++j) c[BA + j] = *(const uint2 *)(pb[j] + 8 * g);
+        for (int i = 0; i < BA; ++i)
+            c[i] = *(const uint2 *)(abase + (oa + 32u * (uint32_t)i * lda + 8u * (uint32_t)g));
         if (LUTSRC != LUT_LDS) {
             const int d = 8 * g + lane8;
             cls = d < D ? P.d_class[d] : 0;
         }
     };
-    // code byte of inner dimension dl (0..7, a compile-time constant) of row r
-    auto code_of = [](const uint2 (&c)[NR], int r, int dl) __attribute__((always_inline)) {
-        return (int)(((dl < 4 ? c[r].x : c[r].y) >> (8 * (dl & 3))) & 0xffu);
+    // a pair starts at an odd group as often as at an even one: 8-byte aligned 16-byte loads
+    struct __attribute__((aligned(8))) pair_t {
+        uint32_t x, y, z, w;
+    };
+    auto load_b = [&](uint4 (&q)[BB], int gp) __attribute__((always_inline)) {
+        const int gl = gp < glast ? gp : glast;
+#pragma unroll
+        for (int j = 0; j < BB; ++j) {
+            const pair_t t =
+                *(const pair_t *)(bbase + (ob + 32u * (uint32_t)j * ldb + 8u * (uint32_t)gl));
+            q[j] = make_uint4(t.x, t.y, t.z, t.w);
+        }
+    };
+    auto shift_of = [&](int gp) __attribute__((always_inline)) {
+        return gp - (gp < glast ? gp : glast);
+    };
+    // code byte of inner dimension dl (0..7, a compile-time constant): A row i of a group,
+    // or B row j of half m (0: first group of the pair, 1: second)
+    auto code_a = [](const uint2 (&c)[BA], int i, int dl) __attribute__((always_inline)) {
+        return (int)(((dl < 4 ? c[i].x : c[i].y) >> (8 * (dl & 3))) & 0xffu);
+    };
+    auto code_b = [](const uint4 (&q)[BB], int m, int j, int dl) __attribute__((always_inline)) {
+        const uint32_t w = dl < 4 ? (m ? q[j].z : q[j].x) : (m ? q[j].w : q[j].y);
+        return (int)((w >> (8 * (dl & 3))) & 0xffu);
     };
 
-    // load unit `unit` of the group whose first d is dg (codes in c) into F
-    auto stage = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&c)[NR], int cls8, int unit,
-                     int dg) __attribute__((always_inline)) {
+    // load unit `unit` of the group whose first d is dg (A codes ca, B codes: half m of qb)
+    auto stage = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&ca)[BA], int cls8,
+                     const uint4 (&qb)[BB], int m, int unit, int dg)
+        __attribute__((always_inline)) {
         const int dl = JPF == 32 ? 2 * unit + h : unit / SPD;    // d within the group
         const int koff = (JPF == 32 ? 0 : 16 * h) + 32 * KSU * (unit % SPD);
 #pragma unroll
         for (int i = 0; i < BA; ++i) {
-            const uint8_t *p = sA + code_of(c, i, dl) * LS + koff;
+            const uint8_t *p = sA + code_a(ca, i, dl) * LS + koff;
 #pragma unroll
             for (int t = 0; t < KSU; ++t) F.a[i][t] = *(const v4i *)(p + 32 * t);
         }
@@ -184,7 +217,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         }
 #pragma unroll
         for (int j = 0; j < BB; ++j) {
-            const uint8_t *p = base + code_of(c, BA + j, dl) * (LUTSRC == LUT_GLOBAL ? ROWB : LS) +
+            const uint8_t *p = base + code_b(qb, m, j, dl) * (LUTSRC == LUT_GLOBAL ? ROWB : LS) +
                                koff;
 #pragma unroll
             for (int t = 0; t < KSU; ++t) F.b[j][t] = *(const v4i *)(p + 32 * t);
@@ -205,15 +238,15 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     };
 
     Fp4Frag<JPF, BA, BB> F0, F1;
-    // one group: its units from `cur`; the last unit stages unit 0 of the next group from
-    // `nxt` and refills `cur` with the group after that (clamped to the last group of the
-    // range, whose codes are then loaded but never used)
-    auto group = [&](uint2 (&cur)[NR], int &ccur, const uint2 (&nxt)[NR], const int &cnxt,
-                     int g) __attribute__((always_inline)) {
+    // one group g (A codes ca, B codes half m of qb); its last unit stages unit 0 of the
+    // next group (A codes can, B codes half mn of qbn), then runs `refill`
+    auto group = [&](const uint2 (&ca)[BA], int cls, const uint4 (&qb)[BB], int m, int g,
+                     const uint2 (&can)[BA], int clsn, const uint4 (&qbn)[BB], int mn,
+                     auto refill) __attribute__((always_inline)) {
         const int dg = 8 * g;
 #pragma unroll
         for (int uu = 0; uu < UPG; uu += 2) {
-            stage(F1, cur, ccur, uu + 1, dg);
+            stage(F1, ca, cls, qb, m, uu + 1, dg);
             mma(F0);
             if (SCHED) {
                 interleave_unit<BA * BB * KSU, NR * KSU, 1>();
@@ -221,10 +254,10 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             }
             done(uu, dg);
             if (uu + 2 < UPG) {
-                stage(F0, cur, ccur, uu + 2, dg);
+                stage(F0, ca, cls, qb, m, uu + 2, dg);
             } else {
-                load_codes(cur, ccur, g + 2 < g1 ? g + 2 : g1 - 1);
-                stage(F0, nxt, cnxt, 0, dg + 8);
+                stage(F0, can, clsn, qbn, mn, 0, dg + 8);
+                refill();
             }
             mma(F1);
             if (SCHED) {
@@ -235,19 +268,34 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         }
     };
 
-    uint2 cx0[NR], cx1[NR];
+    // A: a0 / a1 hold groups of even / odd offset from g0; B: qc holds the pair (g, g+1),
+    // qn the pair (g+2, g+3), in flight
+    uint2 a0[BA], a1[BA];
+    uint4 qc[BB], qn[BB];
     int cl0 = 0, cl1 = 0;
-    load_codes(cx0, cl0, g0);
-    load_codes(cx1, cl1, g0 + 1 < g1 ? g0 + 1 : g1 - 1);
-    stage(F0, cx0, cl0, 0, 8 * g0);
-    // pairs of groups, then an odd last group: the loop body has no branch, so the wait
-    // for a buffer's codes at the top of the loop only covers loads a group old
+    load_a(a0, cl0, g0);
+    load_a(a1, cl1, g0 + 1 < g1 ? g0 + 1 : g1 - 1);
+    load_b(qc, g0);
+    load_b(qn, g0 + 2);
+    int sc = shift_of(g0);                       // 1 only for a lone last group
+    stage(F0, a0, cl0, qc, sc, 0, 8 * g0);
     int g = g0;
+    // full pairs: g + 1 < g1 <= ngroups, so qc's shift is 0; the loop body has no branch
     for (; g + 1 < g1; g += 2) {
-        group(cx0, cl0, cx1, cl1, g);
-        group(cx1, cl1, cx0, cl0, g + 1);
+        const int sn = shift_of(g + 2);
+        group(a0, cl0, qc, 0, g, a1, cl1, qc, 1,
+              [&] { load_a(a0, cl0, g + 2 < g1 ? g + 2 : g1 - 1); });
+        group(a1, cl1, qc, 1, g + 1, a0, cl0, qn, sn, [&] {
+            load_a(a1, cl1, g + 3 < g1 ? g + 3 : g1 - 1);
+#pragma unroll
+            for (int j = 0; j < BB; ++j) qc[j] = qn[j];
+            sc = sn;
+            load_b(qn, g + 4 < g1 ? g + 4 : g1 - 1);
+        });
     }
-    if (g < g1) group(cx0, cl0, cx1, cl1, g);
+    // a lone last group: A codes in a0, B codes half sc of qc (the unit staged for it at the
+    // end of the previous pair used the same half)
+    if (g < g1) group(a0, cl0, qc, sc, g, a1, cl1, qn, 0, [] {});
 }
 
 // Balanced schedule: workgroup c of nwg owns work items [first(c), first(c+1)) of W.
@@ -365,21 +413,16 @@ sc_gemm_fp4_kernel(GemmP P) {
         const int a0 = (ta * WA + wa) * (BA * 32);
         const int b0 = (tb * WB + wb) * (BB * 32);
 
-        const uint8_t *pa[BA];
-        const uint8_t *pb[BB];
-#pragma unroll
-        for (int i = 0; i < BA; ++i)
-            pa[i] = P.ca + batch * P.bsa + (int64_t)(a0 + 32 * i + li) * P.lda;
-#pragma unroll
-        for (int c = 0; c < BB; ++c)
-            pb[c] = P.cb + batch * P.bsb + (int64_t)(b0 + 32 * c + li) * P.ldb;
+        // wave-uniform bases of the wave's first A and B rows
+        const uint8_t *abase = P.ca + batch * P.bsa + (int64_t)a0 * P.lda;
+        const uint8_t *bbase = P.cb + batch * P.bsb + (int64_t)b0 * P.ldb;
 
         v16f acc[BA][BB];
 #pragma unroll
         for (int i = 0; i < BA; ++i)
 #pragma unroll
             for (int c = 0; c < BB; ++c) acc[i][c] = (v16f){0.0f};
-        fp4_accumulate<JPF, BA, BB, LUTSRC, SCHED>(P, sA, sB, pa, pb, g0, g1, h, acc,
+        fp4_accumulate<JPF, BA, BB, LUTSRC, SCHED>(P, sA, sB, abase, bbase, li, g0, g1, h, acc,
                                                     [](int, int) {});
 
         // The lane index, re-read inside the tile loop through an opaque copy: offsets
@@ -558,12 +601,8 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
     const int a0 = (ta * WA + wa) * (BA * 32);
     const int b0 = (tb * WB + wb) * (BB * 32);
 
-    const uint8_t *pa[BA];
-    const uint8_t *pb[BB];
-#pragma unroll
-    for (int i = 0; i < BA; ++i) pa[i] = P.ca + batch * P.bsa + (int64_t)(a0 + 32 * i + li) * P.lda;
-#pragma unroll
-    for (int c = 0; c < BB; ++c) pb[c] = P.cb + batch * P.bsb + (int64_t)(b0 + 32 * c + li) * P.ldb;
+    const uint8_t *abase = P.ca + batch * P.bsa + (int64_t)a0 * P.lda;
+    const uint8_t *bbase = P.cb + batch * P.bsb + (int64_t)b0 * P.ldb;
 
     v16f acc[BA][BB];
     float yac[BA][BB][16];
@@ -607,7 +646,8 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
         }
         ++kchunk;
     };
-    fp4_accumulate<JPF, BA, BB, LUTSRC, false>(P, sA, sB, pa, pb, 0, ngroups, h, acc, after);
+    fp4_accumulate<JPF, BA, BB, LUTSRC, false>(P, sA, sB, abase, bbase, li, 0, ngroups, h, acc,
+                                               after);
 
     // two store loops so that the common one (no row map) issues no loads between stores
     float *__restrict__ ybat = P.y + batch * P.bsy;
