@@ -366,6 +366,32 @@ def test_gemm_int_accumulator(case, impl, tile):
     np.testing.assert_array_equal(got, ref)
 
 
+def _random_gemm_shapes(n):
+    rng = np.random.default_rng(2024)
+    modes = [(256, 256, True), (128, 128, True), (64, 64, False), (16, 16, False)]
+    out = []
+    for k in range(n):
+        N = int(rng.integers(1, 420))
+        M = int(rng.integers(1, 420))
+        # inner dimensions around the split threshold (512) and off multiples of 8 / 16
+        D = int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(500, 1100))]))
+        out.append((N, M, D) + modes[k % len(modes)])
+    return out
+
+
+@pytest.mark.parametrize("case", _random_gemm_shapes(12))
+def test_gemm_random_shapes_fp4(case):
+    """Seeded random shapes through the default (FP4) kernel: whole and split tiles,
+    narrow outputs, lone last groups, inner dimensions off multiples of 8."""
+    N, M, D, L, R, bip = case
+    rng = np.random.default_rng(N + 1000 * M + D)
+    a = rng.standard_normal((N, D)).astype(np.float32)
+    b = rng.standard_normal((M, D)).astype(np.float32)
+    got = _int_accum_gpu(a, b, L=L, R=R, bipolar=bip, impl=2)
+    ref = _int_accum_ref(a, b, L=L, R=R, bipolar=bip)
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_gemm_extremes():
     """Saturated operands: every code at +-Q (full-length Sobol: count = L per d)."""
     N, M, D = 64, 64, 48
