@@ -285,6 +285,7 @@ __global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, 
 constexpr int kGroupThreads = 256;
 constexpr int kGroupMaxRows = 1024;       // row sums of a group live in LDS
 constexpr int kMaxChunks = 16;            // register-held 4-column chunks per thread, max
+constexpr int kBigGroupThreads = 1024;    // threads of a workgroup for groups past 256 x 16
 
 enum { QOP_DIV = 0, QOP_DIVZP = 1, QOP_MUL = 2 };
 
@@ -307,15 +308,27 @@ __device__ __forceinline__ float rne_quotient(float x, float s, float inv, float
     return rne(OP == QOP_DIVZP ? __fadd_rn(t, zp) : t);
 }
 
+// four consecutive floats at a 4-byte aligned address (rows whose stride is not a multiple
+// of 4 floats): still one 16-byte load
+struct __attribute__((aligned(4))) float4u {
+    float x, y, z, w;
+};
+
 template <int SM>
 __device__ __forceinline__ void load_chunk4(const scmp_quant_args &a, int64_t r, int c,
                                             bool vec, float (&v)[4]) {
     const float *row = x_row(a, r);
-    if (vec && c + 4 <= a.cols) {
-        const float4 x4 = *(const float4 *)(row + c);
+    if (c + 4 <= a.cols) {
+        float4 x4;
+        if (vec) {
+            x4 = *(const float4 *)(row + c);
+        } else {
+            const float4u u = *(const float4u *)(row + c);
+            x4 = make_float4(u.x, u.y, u.z, u.w);
+        }
         v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;
         if (SM != SCMP_SMOOTH_NONE) {
-            const float4 s4 = *(const float4 *)(a.smooth + c);
+            const float4u s4 = *(const float4u *)(a.smooth + c);
             const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
             for (int k = 0; k < 4; ++k)
@@ -334,6 +347,7 @@ __device__ __forceinline__ void load_chunk4(const scmp_quant_args &a, int64_t r,
 
 // Workgroup w of nw zeroes its share of the padding rows [cbr, code_rows) of every batch of
 // the code buffer (16-byte stores when the rows allow them), so no separate launch is needed.
+template <int NT>
 __device__ __forceinline__ void zero_pad_share(const scmp_quant_args &a, int64_t cbr, int64_t w,
                                                int64_t nw) {
     const int64_t pad_rows = a.code_rows - cbr;
@@ -346,11 +360,11 @@ __device__ __forceinline__ void zero_pad_share(const scmp_quant_args &a, int64_t
     const int64_t u0 = total * w / nw, u1 = total * (w + 1) / nw;
     int64_t b = (u0 + threadIdx.x) / per;
     int64_t off = (u0 + threadIdx.x) - b * per;
-    for (int64_t u = u0 + threadIdx.x; u < u1; u += kGroupThreads) {
+    for (int64_t u = u0 + threadIdx.x; u < u1; u += NT) {
         uint8_t *dst = a.code + (b * a.code_rows + cbr) * a.code_ld + off * ub;
         if (wide) *(uint4 *)dst = make_uint4(0u, 0u, 0u, 0u);
         else *dst = 0;
-        off += kGroupThreads;
+        off += NT;
         while (off >= per) {
             off -= per;
             ++b;
@@ -359,10 +373,10 @@ __device__ __forceinline__ void zero_pad_share(const scmp_quant_args &a, int64_t
 }
 
 // PT: register-held chunks per thread (npt <= PT); npt > PT re-reads the chunks instead.
-template <int OP, int SM, int PT>
-__global__ void __launch_bounds__(kGroupThreads)
+template <int OP, int SM, int PT, int NT>
+__global__ void __launch_bounds__(NT)
 quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
-    __shared__ uint32_t red0[kGroupThreads / 64], red1[kGroupThreads / 64];
+    __shared__ uint32_t red0[NT / 64], red1[NT / 64];
     __shared__ float rsums[kGroupMaxRows];
     __shared__ uint8_t s_jtab[256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -374,14 +388,14 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
     const bool thermo = a.code && a.code_kind == SCMP_CODE_THERMO;
     const bool lds_jtab = thermo && a.col_class == nullptr;
     if (want_sum)
-        for (int i = tid; i < nr; i += kGroupThreads) rsums[i] = 0.0f;
-    if (lds_jtab) s_jtab[tid] = a.jtab[tid];
+        for (int i = tid; i < nr; i += NT) rsums[i] = 0.0f;
+    if (lds_jtab && tid < 256) s_jtab[tid] = a.jtab[tid];
 
     // position (row, first column) of this thread's k-th chunk, chunk index tid + 256 k;
     // a step of 256 chunks is dr rows and dc chunks
     const int rr_first = tid / cpr;
     const int cc_first = tid - rr_first * cpr;
-    const int dr = kGroupThreads / cpr, dc = kGroupThreads - dr * cpr;
+    const int dr = NT / cpr, dc = NT - dr * cpr;
     auto step_rows = [&](int &cc) __attribute__((always_inline)) {
         cc += dc;
         const bool wrap = cc >= cpr;
@@ -415,7 +429,7 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         int rr = rr_first, cc = cc_first;
 #pragma unroll
         for (int k = 0; k < PT; ++k) {
-            if (k < npt && tid + k * kGroupThreads < nch) {
+            if (k < npt && tid + k * NT < nch) {
                 load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, vals[k]);
                 fold(vals[k], 4 * cc);
             }
@@ -423,7 +437,7 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         }
     } else {
         int rr = rr_first, cc = cc_first;
-        for (int ch = tid; ch < nch; ch += kGroupThreads) {
+        for (int ch = tid; ch < nch; ch += NT) {
             float v[4];
             load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, v);
             fold(v, 4 * cc);
@@ -446,7 +460,7 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
     __syncthreads();
     uint32_t s0 = red0[0], s1 = red1[0];
 #pragma unroll
-    for (int w = 1; w < kGroupThreads / 64; ++w) {
+    for (int w = 1; w < NT / 64; ++w) {
         s0 = s0 > red0[w] ? s0 : red0[w];
         s1 = s1 > red1[w] ? s1 : red1[w];
     }
@@ -550,12 +564,12 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         if (reg) {
 #pragma unroll
             for (int k = 0; k < PT; ++k) {
-                if (k < npt && tid + k * kGroupThreads < nch)
+                if (k < npt && tid + k * NT < nch)
                     emit_fast(vals[k], rr, crow, 4 * cc);
                 advance_code();
             }
         } else {
-            for (int ch = tid; ch < nch; ch += kGroupThreads) {
+            for (int ch = tid; ch < nch; ch += NT) {
                 float v[4];
                 load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, v);
                 emit_fast(v, rr, crow, 4 * cc);
@@ -566,12 +580,12 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         int rr = rr_first, cc = cc_first;
 #pragma unroll
         for (int k = 0; k < PT; ++k) {
-            if (k < npt && tid + k * kGroupThreads < nch) emit(vals[k], rr, 4 * cc);
+            if (k < npt && tid + k * NT < nch) emit(vals[k], rr, 4 * cc);
             advance(rr, cc);
         }
     } else {
         int rr = rr_first, cc = cc_first;
-        for (int ch = tid; ch < nch; ch += kGroupThreads) {
+        for (int ch = tid; ch < nch; ch += NT) {
             float v[4];
             load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, v);
             emit(v, rr, 4 * cc);
@@ -582,15 +596,15 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
     if (a.code) {
         const int c0 = 4 * cpr;
         const int tail = (int)(a.code_ld - c0);
-        for (int e = tid; e < nr * tail; e += kGroupThreads) {
+        for (int e = tid; e < nr * tail; e += NT) {
             const int rr = e / tail, c = c0 + (e - rr * tail);
             const int64_t r = r0 + rr, b = r / cbr, i = r - b * cbr;
             a.code[(b * a.code_rows + i) * a.code_ld + c] = 0;
         }
     }
-    if (a.code) zero_pad_share(a, cbr, blockIdx.x, gridDim.x);
+    if (a.code) zero_pad_share<NT>(a, cbr, blockIdx.x, gridDim.x);
     __syncthreads();
-    for (int rr = tid; rr < nr; rr += kGroupThreads) {
+    for (int rr = tid; rr < nr; rr += NT) {
         const int64_t r = r0 + rr;
         if (a.scale) a.scale[r] = p.s;
         if (a.inv) a.inv[r] = p.inv;
@@ -796,30 +810,40 @@ static int quantize_segments(const scmp_quant_args &a, int64_t segw, int64_t nse
 
 // One workgroup per row group, instantiated for the variant's element operation, the
 // smoothing mode and the register-held chunk count (4: rows up to 4096 columns; 16).
-template <int OP, int PT>
+template <int OP, int PT, int NT = kGroupThreads>
 static void launch_group_pt(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt,
                             bool vec, hipStream_t stream) {
     switch (a.smooth_mode) {
     case SCMP_SMOOTH_DIV:
-        quant_group_kernel<OP, SCMP_SMOOTH_DIV, PT><<<grid, kGroupThreads, 0, stream>>>(
+        quant_group_kernel<OP, SCMP_SMOOTH_DIV, PT, NT><<<grid, NT, 0, stream>>>(
             a, G, cpr, npt, vec);
         break;
     case SCMP_SMOOTH_MUL:
-        quant_group_kernel<OP, SCMP_SMOOTH_MUL, PT><<<grid, kGroupThreads, 0, stream>>>(
+        quant_group_kernel<OP, SCMP_SMOOTH_MUL, PT, NT><<<grid, NT, 0, stream>>>(
             a, G, cpr, npt, vec);
         break;
     default:
-        quant_group_kernel<OP, SCMP_SMOOTH_NONE, PT><<<grid, kGroupThreads, 0, stream>>>(
+        quant_group_kernel<OP, SCMP_SMOOTH_NONE, PT, NT><<<grid, NT, 0, stream>>>(
             a, G, cpr, npt, vec);
         break;
     }
 }
 
+// A group too large for 256 threads' registers takes 1024 threads (multiply-by-reciprocal
+// variants: the per-head attention operands, one group per head), so it is read once.
 template <int OP>
 static void launch_group(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt,
                          bool vec, hipStream_t stream) {
-    if (npt <= 4) launch_group_pt<OP, 4>(a, grid, G, cpr, npt, vec, stream);
-    else launch_group_pt<OP, kMaxChunks>(a, grid, G, cpr, npt, vec, stream);
+    if (npt <= 4) {
+        launch_group_pt<OP, 4>(a, grid, G, cpr, npt, vec, stream);
+    } else if (npt <= kMaxChunks || OP != QOP_MUL) {
+        launch_group_pt<OP, kMaxChunks>(a, grid, G, cpr, npt, vec, stream);
+    } else {
+        const int64_t per = cdiv((int64_t)G * cpr, kBigGroupThreads);
+        const int npt4 = (int)(per <= kMaxChunks ? per : kMaxChunks + 1);
+        launch_group_pt<QOP_MUL, kMaxChunks, kBigGroupThreads>(a, grid, G, cpr, npt4, vec,
+                                                               stream);
+    }
 }
 
 static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stream) {
@@ -829,7 +853,7 @@ static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stre
     const bool vec = (a.ld % 4 == 0) && (((uintptr_t)a.x & 15) == 0) &&
                      (a.smooth_mode == SCMP_SMOOTH_NONE || ((uintptr_t)a.smooth & 15) == 0);
     const dim3 grid((unsigned)ngroups);
-    const int npt = (int)(per <= kMaxChunks ? per : kMaxChunks + 1);
+    const int npt = (int)(per <= kMaxChunks ? per : kMaxChunks + 1);   // at 256 threads
     switch (a.variant) {
     case SCMP_Q_GROUP_SYM:
         launch_group<QOP_DIV>(a, grid, (int)G, (int)cpr, npt, vec, stream);
