@@ -23,6 +23,7 @@ struct GemmP {
     const int8_t *lut;
     const int32_t *d_class;
     int bipolar;
+    int JP;                   // intervals per table row (16 .. 256)
     scmp_epilogue epi;
     float *y;
     int32_t *iout;

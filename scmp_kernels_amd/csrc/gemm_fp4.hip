@@ -70,6 +70,7 @@ static bool fp4_narrow_ok(const scmp_gemm_args &a) { return a.d_class == nullptr
 static int fp4_launch_jpf(const GemmP &P, int64_t batch, int JPF, bool chunked,
                           hipStream_t stream) {
     switch (JPF) {
+    case 16: return gemm_fp4_launch_jpf<16>(P, batch, chunked, stream);
     case 32: return gemm_fp4_launch_jpf<32>(P, batch, chunked, stream);
     case 64: return gemm_fp4_launch_jpf<64>(P, batch, chunked, stream);
     case 128: return gemm_fp4_launch_jpf<128>(P, batch, chunked, stream);
@@ -79,8 +80,10 @@ static int fp4_launch_jpf(const GemmP &P, int64_t batch, int JPF, bool chunked,
 }
 
 int gemm_fp4_run(GemmP &P, const scmp_gemm_args &a, bool chunked, hipStream_t stream) {
-    const int JPF = a.JP < 32 ? 32 : a.JP;
-    if (chunked) return fp4_launch_jpf(P, a.batch, JPF, true, stream);
+    // 16-interval tables: four inner dimensions per MFMA k-step (JPF = 16), except in the
+    // chunk_d kernel, whose chunk boundaries need only be even (JPF = 32)
+    if (chunked) return fp4_launch_jpf(P, a.batch, a.JP < 32 ? 32 : a.JP, true, stream);
+    const int JPF = a.JP;
     Fp4Plan plan = fp4_plan(a.N, a.M, a.D, a.batch, device_cu_count(), fp4_narrow_ok(a));
     P.tile_cols = plan.TC;
     P.tilesA = (int)plan.tilesA;
@@ -111,13 +114,13 @@ __global__ void fp4_lut_kernel(const int8_t *lut, int nclass, int JP, int JPF, u
     const int64_t cr = i / rowb;                       // class * 256 + row
     const int byte = (int)(i - cr * rowb);
     const int u = byte >> 2, pair = byte & 3;          // dword u, nibbles 2*pair, 2*pair + 1
-    const int U4 = JPF / 8, U8 = JP / 4;
+    const int U4 = JP < JPF ? JP / 8 : JPF / 8, U8 = JP / 4;   // dwords holding intervals
     uint32_t out = 0;
     for (int k = 0; k < 2; ++k) {
         const int b = 2 * pair + k;
         const int jp = U4 * b + u;
         int v = 0;
-        if (jp < JP) v = lut[cr * JP + 4 * (jp % U8) + jp / U8];
+        if (u < U4 && jp < JP) v = lut[cr * JP + 4 * (jp % U8) + jp / U8];
         const int mag = v < 0 ? -v : v;
         uint32_t code;
         switch (mag) {

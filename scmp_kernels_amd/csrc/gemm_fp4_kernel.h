@@ -10,11 +10,15 @@
 // inner-dimension ranges add exactly in any order.
 //
 // One MFMA covers K = 64 intervals (lane half h: 32 nibbles = 4 dwords). Layout of one
-// JPF-nibble table row: dword u (JPF/8 of them), nibble b holds interval j' = (JPF/8)*b + u;
-// k-step t, lane half h holds dwords u = 8t + 4h + w. JPF = 32 puts two inner dimensions in
-// one k-step (half h takes d = 2p + h); smaller tables are padded to 32. Both operands are
-// rows of tables in LDS selected by a code byte: the A thermometer table (row = THERMO
-// code) and the stream table (row = B code), so the inner loop is LDS reads and MFMAs.
+// table row of JP intervals (JP >= 32): dword u (JP/8 of them), nibble b holds interval
+// j' = (JP/8)*b + u; k-step t, lane half h holds dwords u = 8t + 4h + w. JPF = 32 puts two
+// inner dimensions in one k-step (half h takes d = 2p + h). A 16-interval table is stored
+// in 32-interval rows: dwords 0-1 hold j' = 2b + u, dwords 2-3 are zero; JPF = 16 reads
+// just those 8 bytes for two inner dimensions per lane half, four per k-step (half h takes
+// d = 4p + 2h and 4p + 2h + 1), while the chunk_d kernel reads such rows whole (JPF = 32).
+// Both operands are rows of tables in LDS selected by a code byte: the A thermometer table
+// (row = THERMO code) and the stream table (row = B code), so the inner loop is LDS reads
+// and MFMAs.
 //
 // Two kernels:
 //  * sc_gemm_fp4_kernel — persistent and balanced. The work is the list of (tile, group of
@@ -55,12 +59,13 @@ constexpr int kXcds = 8;
 
 template <int JPF>
 struct Fp4Geom {
-    static constexpr int ROWB = JPF / 2;                         // bytes per table row
+    static constexpr int ROWB = (JPF < 32 ? 32 : JPF) / 2;      // bytes per stored table row
     static constexpr int KS = JPF >= 64 ? JPF / 64 : 1;          // MFMA k-steps per d
-    // pipeline unit: KSU k-steps of one d (two d for JPF = 32); SPD units per d
+    // pipeline unit: KSU k-steps of one d (two d for JPF = 32, four for 16); SPD units per d
     static constexpr int KSU = KS > 2 ? 2 : KS;
     static constexpr int SPD = KS / KSU;
-    static constexpr int UPG = JPF == 32 ? 4 : 8 * SPD;          // units per 8 codes
+    static constexpr int DPU = JPF == 16 ? 4 : JPF == 32 ? 2 : 1;    // d per unit (<= 1 k-step)
+    static constexpr int UPG = JPF <= 32 ? 8 / DPU : 8 * SPD;        // units per 8 codes
     // odd number of 16-byte chunks between LDS rows: spreads rows over the bank groups
     static constexpr int LS = 16 * ((ROWB / 16) | 1);
     static constexpr int TAB = 256 * LS;                          // one table in LDS
@@ -96,16 +101,19 @@ __device__ __forceinline__ int fp4_tables_bytes(const GemmP &P) {
 template <int JPF, int LUTSRC, int NT>
 __device__ __forceinline__ void fp4_load_tables(const GemmP &P, uint8_t *sA, uint8_t *sB) {
     using G = Fp4Geom<JPF>;
-    constexpr int U = JPF / 8;                 // dwords per row
+    constexpr int U = G::ROWB / 4;             // dwords per stored row (8 intervals each)
+    const int Ut = P.JP < 8 * U ? P.JP / 8 : U; // dwords holding intervals (JP = 16: 2)
     const int tid = threadIdx.x;
     for (int e = tid; e < 256 * U; e += NT) {
         const int row = e / U, u = e - row * U;
         const int j = P.bipolar ? (row & 0x7f) : row;
         const uint32_t one = (P.bipolar && (row & 0x80)) ? 0xAu : 0x2u;
         uint32_t w = 0;
+        if (u < Ut) {
 #pragma unroll
-        for (int b = 0; b < 8; ++b)
-            if (U * b + u < j) w |= one << (4 * b);
+            for (int b = 0; b < 8; ++b)
+                if (Ut * b + u < j) w |= one << (4 * b);
+        }
         *(uint32_t *)(sA + row * G::LS + 4 * u) = w;
     }
     if (LUTSRC != LUT_GLOBAL) {
@@ -191,10 +199,43 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         return (int)((w >> (8 * (dl & 3))) & 0xffu);
     };
 
+    // JPF = 16: the lane half's two inner dimensions dl, dl + 1 of a unit, 8 bytes (16
+    // intervals) of a table row each, side by side in one fragment
+    auto stage16 = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&ca)[BA], int cls8,
+                       const uint4 (&qb)[BB], int m, int unit) __attribute__((always_inline)) {
+        const int dl = 4 * unit + 2 * h;
+#pragma unroll
+        for (int i = 0; i < BA; ++i) {
+            const uint2 r0 = *(const uint2 *)(sA + code_a(ca, i, dl) * LS);
+            const uint2 r1 = *(const uint2 *)(sA + code_a(ca, i, dl + 1) * LS);
+            F.a[i][0] = (v4i){(int)r0.x, (int)r0.y, (int)r1.x, (int)r1.y};
+        }
+        const uint8_t *base0 = sB, *base1 = sB;
+        if (LUTSRC != LUT_LDS) {
+            const int c0 = __builtin_amdgcn_readlane(cls8, 4 * unit);
+            const int c1 = __builtin_amdgcn_readlane(cls8, 4 * unit + 1);
+            const int c2 = __builtin_amdgcn_readlane(cls8, 4 * unit + 2);
+            const int c3 = __builtin_amdgcn_readlane(cls8, 4 * unit + 3);
+            const int k0 = h ? c2 : c0, k1 = h ? c3 : c1;
+            base0 = LUTSRC == LUT_GLOBAL ? glut + (int64_t)k0 * 256 * ROWB : sB + k0 * TAB;
+            base1 = LUTSRC == LUT_GLOBAL ? glut + (int64_t)k1 * 256 * ROWB : sB + k1 * TAB;
+        }
+        constexpr int RS = LUTSRC == LUT_GLOBAL ? ROWB : LS;
+#pragma unroll
+        for (int j = 0; j < BB; ++j) {
+            const uint2 r0 = *(const uint2 *)(base0 + code_b(qb, m, j, dl) * RS);
+            const uint2 r1 = *(const uint2 *)(base1 + code_b(qb, m, j, dl + 1) * RS);
+            F.b[j][0] = (v4i){(int)r0.x, (int)r0.y, (int)r1.x, (int)r1.y};
+        }
+    };
     // load unit `unit` of the group whose first d is dg (A codes ca, B codes: half m of qb)
     auto stage = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&ca)[BA], int cls8,
                      const uint4 (&qb)[BB], int m, int unit, int dg)
         __attribute__((always_inline)) {
+        if constexpr (JPF == 16) {
+            stage16(F, ca, cls8, qb, m, unit);
+            return;
+        }
         const int dl = JPF == 32 ? 2 * unit + h : unit / SPD;    // d within the group
         const int koff = (JPF == 32 ? 0 : 16 * h) + 32 * KSU * (unit % SPD);
 #pragma unroll
@@ -225,7 +266,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     };
     auto done = [&](int unit, int dg) __attribute__((always_inline)) {
         if (unit % SPD != SPD - 1) return;
-        if (JPF == 32) after(dg + 2 * unit, dg + 2 * unit + 1);
+        if (JPF <= 32) after(dg + G::DPU * unit, dg + G::DPU * unit + G::DPU - 1);
         else after(dg + unit / SPD, dg + unit / SPD);
     };
     auto mma = [&](const Fp4Frag<JPF, BA, BB> &F) __attribute__((always_inline)) {
@@ -249,7 +290,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             stage(F1, ca, cls, qb, m, uu + 1, dg);
             mma(F0);
             if (SCHED) {
-                interleave_unit<BA * BB * KSU, NR * KSU, 1>();
+                interleave_unit<BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1), 1>();
                 __builtin_amdgcn_sched_barrier(0);
             }
             done(uu, dg);
@@ -261,7 +302,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             }
             mma(F1);
             if (SCHED) {
-                interleave_unit<BA * BB * KSU, NR * KSU, 1>();
+                interleave_unit<BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1), 1>();
                 __builtin_amdgcn_sched_barrier(0);
             }
             done(uu + 1, dg);
@@ -747,17 +788,30 @@ static int launch_fp4_chunked(const GemmP &P0, int64_t batch, hipStream_t stream
 template <int JPF>
 int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t s) {
     using G = Fp4Geom<JPF>;
+    if constexpr (JPF == 16) {
+        if (chunked) {                           // the chunk_d kernel takes such tables as 32
+            set_error("scmp_sc_gemm(fp4): chunked launch with JPF=16");
+            return SCMP_E_ARG;
+        }
+    }
     const int64_t stage = kFactorFloats * (int64_t)sizeof(float);
     if (P.d_class == nullptr) {
-        if (chunked) return launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s);
+        if constexpr (JPF != 16)
+            if (chunked) return launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s);
         return P.tile_cols == 64 ? launch_fp4_main<JPF, LUT_LDS, true>(P, batch, s)
                                  : launch_fp4_main<JPF, LUT_LDS>(P, batch, s);
     }
-    if (P.nclass > 0 && (int64_t)G::TAB * (1 + P.nclass) + stage <= kFp4MaxLds)
-        return chunked ? launch_fp4_chunked<JPF, LUT_LDS_CLASSES>(P, batch, s)
-                       : launch_fp4_main<JPF, LUT_LDS_CLASSES>(P, batch, s);
-    return chunked ? launch_fp4_chunked<JPF, LUT_GLOBAL>(P, batch, s)
-                   : launch_fp4_main<JPF, LUT_GLOBAL>(P, batch, s);
+    if constexpr (JPF == 16) {
+        if (P.nclass > 0 && (int64_t)G::TAB * (1 + P.nclass) + stage <= kFp4MaxLds)
+            return launch_fp4_main<JPF, LUT_LDS_CLASSES>(P, batch, s);
+        return launch_fp4_main<JPF, LUT_GLOBAL>(P, batch, s);
+    } else {
+        if (P.nclass > 0 && (int64_t)G::TAB * (1 + P.nclass) + stage <= kFp4MaxLds)
+            return chunked ? launch_fp4_chunked<JPF, LUT_LDS_CLASSES>(P, batch, s)
+                           : launch_fp4_main<JPF, LUT_LDS_CLASSES>(P, batch, s);
+        return chunked ? launch_fp4_chunked<JPF, LUT_GLOBAL>(P, batch, s)
+                       : launch_fp4_main<JPF, LUT_GLOBAL>(P, batch, s);
+    }
 }
 
 }  // namespace scmp

@@ -482,7 +482,7 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     P.cb = a.cb; P.ldb = a.ldb; P.bsb = a.bsb;
     P.N = (int)a.N; P.M = (int)a.M; P.D = (int)a.D;
     P.chunk = chunked ? (int)a.chunk : 0;
-    P.lut = a.lut; P.d_class = a.d_class; P.bipolar = a.bipolar;
+    P.lut = a.lut; P.d_class = a.d_class; P.bipolar = a.bipolar; P.JP = a.JP;
     P.epi = a.epi; P.y = a.y; P.ldy = a.ldy; P.bsy = a.bsy;
     P.row_map = a.row_map;
     P.tilesA = 0;
