@@ -440,6 +440,9 @@ RANDOM_CASES = [
     ("per_row", dict(mode="unipolar", group_a=4, group_b=3, stoc_len=16, rng_levels=16),
      (50, 40, 64)),
     ("per_row", dict(mode="bipolar", chunk_d=72), (300, 65, 3 * 72 + 48)),
+    # 16-interval tables through the chunk_d kernel (stored in 32-interval rows)
+    ("per_row", dict(mode="bipolar", chunk_d=24, stoc_len=16), (90, 70, 5 * 24 + 10)),
+    ("per_row", dict(mode="bipolar", chunk_d=26, stoc_len=16, rng_levels=16), (70, 90, 4 * 26)),
     ("per_row", dict(mode="bipolar", halve_bipolar_stoc_len=True), (64, 64, 128)),
     ("per_tensor", dict(mode="bipolar"), (32, 64, 256)),
     ("per_tensor", dict(mode="unipolar"), (40, 33, 100)),
