@@ -29,7 +29,8 @@ extern "C" {
 #define SCMP_E_LAUNCH (-2)
 #define SCMP_E_UNSUPPORTED (-3)
 
-/* Library identification and the last error message of the calling thread. */
+/* Library identification and the last error message of the calling thread. Version 2:
+ * scmp_quant_args.row_index, scmp_gemm_args.row_map and scmp_gemm_args.group_class. */
 int scmp_abi_version(void);
 const char *scmp_last_error(void);
 
@@ -225,6 +226,12 @@ typedef struct scmp_gemm_args {
     int64_t workspace_bytes;
     const int64_t *row_map;    /* output row of A row n (y / iout row row_map[n], each a valid
                                   output row): scatters a row subset in place; NULL: n */
+    const int32_t *group_class; /* FP4, not chunked: class of each group of 8 code columns
+                                  (D / 8 rounded up entries, D a multiple of 8), every column
+                                  of a group in that class; the kernel stages a class table
+                                  in LDS where the class changes (codes laid out by class
+                                  runs: scmp_permute_code_columns). d_class must be NULL.
+                                  NULL: no grouping */
 } scmp_gemm_args;
 
 int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream);
@@ -237,11 +244,21 @@ int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream);
 int64_t scmp_sc_gemm_workspace_bytes(const scmp_gemm_args *args);
 
 /* FP4 (e2m1) form of a stream table for SCMP_GEMM_MFMA_FP4: JPF = max(JP, 32) nibbles per
- * row (JPF / 2 bytes), dword u nibble b holds interval j' = (JPF/8)*b + u. Counts that e2m1
- * cannot represent exactly (anything but 0, 1, 2, 3, 4, 6) set *bad to 1; the table is then
- * unusable and the int8 kernel must be used. */
+ * row (JPF / 2 bytes), dword u nibble b holds interval j' = (JP/8)*b + u (JP = 16: dwords 0
+ * and 1, dwords 2 and 3 zero). Counts that e2m1 cannot represent exactly (anything but 0, 1,
+ * 2, 3, 4, 6) set *bad to 1; the table is then unusable and the int8 kernel must be used. */
 int scmp_build_fp4_lut(const int8_t *lut, int nclass, int JP, uint8_t *lut4, int32_t *bad,
                        hipStream_t stream);
+
+/* Code columns rearranged into class runs for scmp_gemm_args.group_class: out[r][p] =
+ * in[r][src[p]] for src[p] >= 0, 0 for src[p] < 0 (padding of a run to whole groups of 8)
+ * and for ncols <= p < ld_out; rows 0..rows-1 of both buffers; every src[p] < ld_in (not
+ * checked: src is device memory), ld_out a multiple of 16. No counterpart in the
+ * reference (it reads each d's table through the d's class in its tiled kernel,
+ * scmp_kernels/sc/kernels.py:176-252). */
+int scmp_permute_code_columns(const uint8_t *in, int64_t rows, int64_t ld_in,
+                              const int32_t *src, int64_t ncols, uint8_t *out, int64_t ld_out,
+                              hipStream_t stream);
 
 /* Bit planes of a stream table for SCMP_GEMM_VALU: bitlut[c][row][plane][w] bit u of
  * word w is bit `plane` of |lut[c][row][j']| for j' = 32w + u (logical interval order). */

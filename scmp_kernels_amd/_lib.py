@@ -64,6 +64,7 @@ class GemmArgs(ctypes.Structure):
         ("epi", Epilogue), ("y", c_vp), ("iout", c_vp), ("ldy", c_i64), ("bsy", c_i64),
         ("impl", c_int), ("bitlut", c_vp), ("tile", c_int), ("nclass", c_int),
         ("workspace", c_vp), ("workspace_bytes", c_i64), ("row_map", c_vp),
+        ("group_class", c_vp),
     ]
 
 
@@ -71,7 +72,7 @@ EXPORTS = [
     "scmp_abi_version", "scmp_last_error", "scmp_rng_sobol", "scmp_rng_lfsr",
     "scmp_rng_expand", "scmp_rng_prepare", "scmp_lfsr_search", "scmp_build_stream_tables",
     "scmp_quant_workspace_bytes", "scmp_quantize", "scmp_sc_gemm", "scmp_build_bitlut",
-    "scmp_build_fp4_lut", "scmp_sc_gemm_workspace_bytes",
+    "scmp_build_fp4_lut", "scmp_sc_gemm_workspace_bytes", "scmp_permute_code_columns",
 ]
 
 _lib = None
@@ -109,6 +110,8 @@ def load(path: str = LIB_PATH):
         lib.scmp_sc_gemm_workspace_bytes.restype = c_i64
         lib.scmp_build_bitlut.argtypes = [c_vp, c_int, c_int, c_vp, c_vp]
         lib.scmp_build_fp4_lut.argtypes = [c_vp, c_int, c_int, c_vp, c_vp, c_vp]
+        lib.scmp_permute_code_columns.argtypes = [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64,
+                                                  c_vp]
         for name in EXPORTS:
             getattr(lib, name).restype = getattr(lib, name).restype or c_int
         lib.scmp_last_error.restype = ctypes.c_char_p

@@ -40,6 +40,7 @@ struct GemmP {
     float *part;
     int *cnt;
     const int64_t *row_map;   // output row of A row n (NULL: n)
+    const int32_t *group_class;   // FP4: class of each 8-d group (NULL: none)
 };
 
 // Output row of A row n: the caller's row map scatters a row subset in place.

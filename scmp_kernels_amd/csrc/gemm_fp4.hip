@@ -65,7 +65,9 @@ __global__ void zero_ints_kernel(int *p, int64_t n) {
 }
 
 // Narrow tiles are instantiated for a single stream table in LDS (no per-d classes).
-static bool fp4_narrow_ok(const scmp_gemm_args &a) { return a.d_class == nullptr; }
+static bool fp4_narrow_ok(const scmp_gemm_args &a) {
+    return a.d_class == nullptr && a.group_class == nullptr;
+}
 
 static int fp4_launch_jpf(const GemmP &P, int64_t batch, int JPF, bool chunked,
                           hipStream_t stream) {
@@ -148,6 +150,93 @@ extern "C" int64_t scmp_sc_gemm_workspace_bytes(const scmp_gemm_args *a) {
         return 0;
     const Fp4Plan p = fp4_plan(a->N, a->M, a->D, a->batch, device_cu_count(), fp4_narrow_ok(*a));
     return p.split ? p.cnt_bytes + p.part_bytes : 0;
+}
+
+// Code columns in class runs, any row stride: thread (r, 16-byte chunk p0) writes
+// out[r][p0 .. p0 + 15] from bytes of row r read through the cache.
+__global__ void permute_columns_kernel(const uint8_t *in, int64_t rows, int64_t ld_in,
+                                       const int32_t *src, int64_t ncols, uint8_t *out,
+                                       int64_t ld_out) {
+    const int64_t chunks = ld_out / 16;
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i >= rows * chunks) return;
+    const int64_t r = i / chunks, p0 = 16 * (i - r * chunks);
+    const uint8_t *row = in + r * ld_in;
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int64_t p = p0 + k;
+        const int32_t c = p < ncols ? src[p] : -1;
+        if (c >= 0) w[k >> 2] |= (uint32_t)row[c] << (8 * (k & 3));
+    }
+    *(uint4 *)(out + r * ld_out + p0) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Row strides that are multiples of 16 (code buffers): RW rows per workgroup are read
+// whole into LDS with 16-byte loads, then each thread gathers 16-byte output chunks from
+// LDS, reading its 16 source indices once for the RW rows.
+template <int RW>
+__global__ void __launch_bounds__(256)
+permute_columns_lds_kernel(const uint8_t *in, int64_t rows, int64_t ld_in, const int32_t *src,
+                           int64_t ncols, uint8_t *out, int64_t ld_out) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t srow[];
+    const int64_t r0 = (int64_t)blockIdx.x * RW;
+    const int nr = rows - r0 < RW ? (int)(rows - r0) : RW;
+    const int cin = (int)(ld_in / 16);
+    for (int e = threadIdx.x; e < nr * cin; e += 256) {
+        const int k = e / cin, c = e - k * cin;
+        *(uint4 *)(srow + (int64_t)k * ld_in + 16 * c) =
+            *(const uint4 *)(in + (r0 + k) * ld_in + 16 * c);
+    }
+    __syncthreads();
+    const int cout = (int)(ld_out / 16);
+    for (int c = threadIdx.x; c < cout; c += 256) {
+        const int64_t p0 = 16 * (int64_t)c;
+        int32_t s[16];
+        if (p0 + 16 <= ncols) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int4 v = *(const int4 *)(src + p0 + 4 * q);
+                s[4 * q] = v.x; s[4 * q + 1] = v.y; s[4 * q + 2] = v.z; s[4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) s[k] = p0 + k < ncols ? src[p0 + k] : -1;
+        }
+        for (int k = 0; k < nr; ++k) {
+            const uint8_t *row = srow + (int64_t)k * ld_in;
+            uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (s[j] >= 0) w[j >> 2] |= (uint32_t)row[s[j]] << (8 * (j & 3));
+            *(uint4 *)(out + (r0 + k) * ld_out + p0) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+}
+
+extern "C" int scmp_permute_code_columns(const uint8_t *in, int64_t rows, int64_t ld_in,
+                                         const int32_t *src, int64_t ncols, uint8_t *out,
+                                         int64_t ld_out, hipStream_t stream) {
+    SCMP_REQUIRE(in && src && out, "scmp_permute_code_columns: null pointer");
+    SCMP_REQUIRE(rows > 0 && ncols > 0 && ld_in > 0 && ld_out % 16 == 0 && ld_out >= ncols,
+                 "scmp_permute_code_columns: rows=%lld ncols=%lld ld_in=%lld ld_out=%lld "
+                 "(ld_out a multiple of 16, >= ncols)", (long long)rows, (long long)ncols,
+                 (long long)ld_in, (long long)ld_out);
+    const bool aligned = ld_in % 16 == 0 && ((uintptr_t)in & 15) == 0 &&
+                         ((uintptr_t)out & 15) == 0 && ((uintptr_t)src & 15) == 0;
+    if (aligned && ld_in <= 16384) {
+        permute_columns_lds_kernel<4><<<cdiv(rows, 4), 256, 4 * ld_in, stream>>>(
+            in, rows, ld_in, src, ncols, out, ld_out);
+    } else if (aligned && ld_in <= 65536) {
+        permute_columns_lds_kernel<1><<<rows, 256, ld_in, stream>>>(in, rows, ld_in, src, ncols,
+                                                                   out, ld_out);
+    } else {
+        const int64_t n = rows * (ld_out / 16);
+        permute_columns_kernel<<<cdiv(n, 256), 256, 0, stream>>>(in, rows, ld_in, src, ncols,
+                                                                 out, ld_out);
+    }
+    SCMP_LAUNCH_CHECK("scmp_permute_code_columns");
+    return SCMP_OK;
 }
 
 extern "C" int scmp_build_fp4_lut(const int8_t *lut, int nclass, int JP, uint8_t *lut4,

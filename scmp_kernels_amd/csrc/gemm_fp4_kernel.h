@@ -47,8 +47,10 @@ __device__ __forceinline__ v16f mfma_fp4(v4i a, v4i b, v16f c) {
 }
 
 // Where the stream tables live: one table in LDS, every class table in LDS (per-d
-// classes, when they fit), or per-class tables read from global memory.
-enum { LUT_LDS = 0, LUT_LDS_CLASSES = 1, LUT_GLOBAL = 2 };
+// classes, when they fit), per-class tables read from global memory, or one class table
+// at a time in LDS, replaced where the class of the 8-d groups changes (inner dimensions
+// laid out in runs of one class).
+enum { LUT_LDS = 0, LUT_LDS_CLASSES = 1, LUT_GLOBAL = 2, LUT_RUNS = 3 };
 
 // floats of the per-tile epilogue area of a 256 x 256 tile: 3 factors per row and per
 // column, then one int64 output offset per row (two floats' worth each)
@@ -93,11 +95,14 @@ __device__ __forceinline__ void interleave_unit() {
 template <int JPF, int LUTSRC>
 __device__ __forceinline__ int fp4_tables_bytes(const GemmP &P) {
     using G = Fp4Geom<JPF>;
-    return G::TAB * (1 + (LUTSRC == LUT_LDS ? 1 : LUTSRC == LUT_LDS_CLASSES ? P.nclass : 0));
+    return G::TAB * (1 + (LUTSRC == LUT_LDS || LUTSRC == LUT_RUNS ? 1
+                          : LUTSRC == LUT_LDS_CLASSES                ? P.nclass
+                                                                     : 0));
 }
 
 // Prologue: the thermometer table T[code][j'] = sign(code) if j' < j(code) else 0 (rows =
-// THERMO code byte: bipolar sign bit | j, unipolar j), and the stream table(s) copied in.
+// THERMO code byte: bipolar sign bit | j, unipolar j), and the stream table(s) copied in
+// (LUT_RUNS: by the accumulation loop, per run).
 template <int JPF, int LUTSRC, int NT>
 __device__ __forceinline__ void fp4_load_tables(const GemmP &P, uint8_t *sA, uint8_t *sB) {
     using G = Fp4Geom<JPF>;
@@ -116,7 +121,7 @@ __device__ __forceinline__ void fp4_load_tables(const GemmP &P, uint8_t *sA, uin
         }
         *(uint32_t *)(sA + row * G::LS + 4 * u) = w;
     }
-    if (LUTSRC != LUT_GLOBAL) {
+    if (LUTSRC == LUT_LDS || LUTSRC == LUT_LDS_CLASSES) {
         constexpr int CH = G::ROWB / 16;         // 16-byte chunks per row
         const int rows = (LUTSRC == LUT_LDS_CLASSES ? P.nclass : 1) * 256;
         const v4i *src = (const v4i *)P.lut;
@@ -151,6 +156,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     constexpr int ROWB = G::ROWB, KSU = G::KSU, SPD = G::SPD, UPG = G::UPG, LS = G::LS,
                   TAB = G::TAB;
     constexpr int NR = BA + BB;                  // code rows per lane: A rows, then B rows
+    constexpr bool PERD = LUTSRC == LUT_LDS_CLASSES || LUTSRC == LUT_GLOBAL;   // per-d classes
     const uint8_t *glut = (const uint8_t *)P.lut;
     const int D = P.D;
     const int ngroups = (D + 7) / 8;
@@ -168,9 +174,16 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
 #pragma unroll
         for (int i = 0; i < BA; ++i)
             c[i] = *(const uint2 *)(abase + (oa + 32u * (uint32_t)i * lda + 8u * (uint32_t)g));
-        if (LUTSRC != LUT_LDS) {
+        if (PERD) {
             const int d = 8 * g + lane8;
             cls = d < D ? P.d_class[d] : 0;
+        }
+        if (LUTSRC == LUT_RUNS) {
+            // the group's class, by a vector load issued after the codes: waiting for it
+            // waits for nothing that is not needed at the same point
+            int z = 0;
+            asm volatile("" : "+v"(z));
+            cls = P.group_class[g + z];
         }
     };
     // a pair starts at an odd group as often as at an even one: 8-byte aligned 16-byte loads
@@ -211,7 +224,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             F.a[i][0] = (v4i){(int)r0.x, (int)r0.y, (int)r1.x, (int)r1.y};
         }
         const uint8_t *base0 = sB, *base1 = sB;
-        if (LUTSRC != LUT_LDS) {
+        if (PERD) {
             const int c0 = __builtin_amdgcn_readlane(cls8, 4 * unit);
             const int c1 = __builtin_amdgcn_readlane(cls8, 4 * unit + 1);
             const int c2 = __builtin_amdgcn_readlane(cls8, 4 * unit + 2);
@@ -245,7 +258,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             for (int t = 0; t < KSU; ++t) F.a[i][t] = *(const v4i *)(p + 32 * t);
         }
         const uint8_t *base = sB;
-        if (LUTSRC != LUT_LDS) {
+        if (PERD) {
             int cls;
             if (JPF == 32) {                     // the lane halves take d = 2 unit + h
                 const int c0 = __builtin_amdgcn_readlane(cls8, 2 * unit);
@@ -278,6 +291,22 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
                 for (int j = 0; j < BB; ++j) acc[i][j] = mfma_fp4(F.a[i][t], F.b[j][t], acc[i][j]);
     };
 
+    // LUT_RUNS: the table of class c (clamped to the valid classes) replaces the one in LDS
+    // once every wave is done reading it; the whole workgroup runs the same groups, so every
+    // wave reaches the same barriers
+    auto run_table = [&](int c) __attribute__((always_inline)) {
+        c = c < 0 ? 0 : c >= P.nclass ? P.nclass - 1 : c;
+        constexpr int CH = ROWB / 16;
+        const v4i *src = (const v4i *)(glut + (int64_t)c * 256 * ROWB);
+        uint8_t *dst = (uint8_t *)sB;
+        __syncthreads();
+        for (int e = (int)threadIdx.x; e < 256 * CH; e += (int)blockDim.x) {
+            const int row = e / CH, col = e - row * CH;
+            *(v4i *)(dst + row * LS + 16 * col) = src[e];
+        }
+        __syncthreads();
+    };
+
     Fp4Frag<JPF, BA, BB> F0, F1;
     // one group g (A codes ca, B codes half m of qb); its last unit stages unit 0 of the
     // next group (A codes can, B codes half mn of qbn), then runs `refill`
@@ -297,6 +326,10 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             if (uu + 2 < UPG) {
                 stage(F0, ca, cls, qb, m, uu + 2, dg);
             } else {
+                if (LUTSRC == LUT_RUNS) {
+                    const int cn = __builtin_amdgcn_readfirstlane(clsn);
+                    if (cn != __builtin_amdgcn_readfirstlane(cls)) run_table(cn);
+                }
                 stage(F0, can, clsn, qbn, mn, 0, dg + 8);
                 refill();
             }
@@ -319,6 +352,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     load_b(qc, g0);
     load_b(qn, g0 + 2);
     int sc = shift_of(g0);                       // 1 only for a lone last group
+    if (LUTSRC == LUT_RUNS) run_table(__builtin_amdgcn_readfirstlane(cl0));
     stage(F0, a0, cl0, qc, sc, 0, 8 * g0);
     int g = g0;
     // full pairs: g + 1 < g1 <= ngroups, so qc's shift is 0; the loop body has no branch
@@ -740,7 +774,9 @@ static int fp4_set_lds(K kern, size_t lds) {
 template <int JPF, int LUTSRC>
 static size_t fp4_tables_bytes_host(const GemmP &P) {
     using G = Fp4Geom<JPF>;
-    return (size_t)G::TAB * (1 + (LUTSRC == LUT_LDS ? 1 : LUTSRC == LUT_LDS_CLASSES ? P.nclass : 0));
+    return (size_t)G::TAB * (1 + (LUTSRC == LUT_LDS || LUTSRC == LUT_RUNS ? 1
+                                  : LUTSRC == LUT_LDS_CLASSES                ? P.nclass
+                                                                             : 0));
 }
 
 // Non-chunked: 256 x 256 tiles, each wave 128 x 128 (4 x 4 blocks of 32 x 32), or narrow
@@ -795,6 +831,14 @@ int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t
         }
     }
     const int64_t stage = kFactorFloats * (int64_t)sizeof(float);
+    if (P.group_class != nullptr) {
+        if (chunked || P.d_class != nullptr || P.nclass <= 0) {
+            set_error("scmp_sc_gemm(fp4): group_class needs a non-chunked launch, no d_class "
+                      "and nclass > 0");
+            return SCMP_E_ARG;
+        }
+        return launch_fp4_main<JPF, LUT_RUNS>(P, batch, s);
+    }
     if (P.d_class == nullptr) {
         if constexpr (JPF != 16)
             if (chunked) return launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s);

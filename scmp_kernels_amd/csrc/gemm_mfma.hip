@@ -474,6 +474,11 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
                  "scmp_sc_gemm: chunked accumulation needs the ROWCOL epilogue");
     SCMP_REQUIRE(!chunked || a.impl != SCMP_GEMM_VALU,
                  "scmp_sc_gemm: chunked accumulation is implemented by the MFMA kernels");
+    SCMP_REQUIRE(a.group_class == nullptr ||
+                     (a.impl == SCMP_GEMM_MFMA_FP4 && !chunked && a.d_class == nullptr &&
+                      a.D % 8 == 0 && a.nclass > 0),
+                 "scmp_sc_gemm: group_class needs the FP4 kernel, no chunked accumulation, "
+                 "no d_class, D a multiple of 8 and nclass > 0");
     if (a.impl == SCMP_GEMM_VALU) return gemm_valu_launch(a, stream);
     SCMP_REQUIRE(a.impl == SCMP_GEMM_MFMA || a.impl == SCMP_GEMM_MFMA_FP4,
                  "scmp_sc_gemm: unknown impl %d", a.impl);
@@ -485,6 +490,7 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     P.lut = a.lut; P.d_class = a.d_class; P.bipolar = a.bipolar; P.JP = a.JP;
     P.epi = a.epi; P.y = a.y; P.ldy = a.ldy; P.bsy = a.bsy;
     P.row_map = a.row_map;
+    P.group_class = a.group_class;
     P.tilesA = 0;
     P.tile_cols = 256;
     P.nclass = a.nclass;

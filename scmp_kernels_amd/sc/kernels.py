@@ -147,18 +147,45 @@ def _gemm_impl() -> Optional[int]:
             "fp4": _lib.GEMM_MFMA_FP4}.get(v)
 
 
+# LDS of one FP4 GEMM workgroup (gemm_fp4_kernel.h: kFp4MaxLds, kFactorFloats)
+_FP4_MAX_LDS = 160 * 1024
+_FP4_STAGE_BYTES = (6 * 256 + 2 * 256) * 4
+
+
+def _fp4_class_runs(tabs: "_tables.StreamTables", D: int):
+    """The class-run layout (StreamTables.class_runs) when the FP4 kernel should use it:
+    several classes whose tables do not all fit in LDS, and runs padded by at most an
+    eighth of D. SCMP_FP4_RUNS=0 keeps the per-d global-table path, =1 takes runs
+    whenever they are legal."""
+    env = os.environ.get("SCMP_FP4_RUNS", "")
+    if env == "0" or tabs.nclass <= 1 or D != tabs.D:
+        return None
+    rowb = max(tabs.JP, 32) // 2
+    tab = 256 * 16 * ((rowb // 16) | 1)          # one table in LDS (padded rows)
+    if env != "1" and tab * (1 + tabs.nclass) + _FP4_STAGE_BYTES <= _FP4_MAX_LDS:
+        return None                              # every class table fits in LDS
+    runs = tabs.class_runs()
+    if env != "1" and runs[2] > D + D // 8:
+        return None
+    return runs
+
+
+def _permute_codes(c: torch.Tensor, src: torch.Tensor, Dp: int, stream) -> torch.Tensor:
+    """Code buffer with its columns in class-run order (scmp_permute_code_columns)."""
+    shape = tuple(c.shape[:-1]) + (_round_up(Dp, 16),)
+    out = torch.empty(shape, dtype=torch.uint8, device=c.device)
+    rows = c.numel() // c.shape[-1]
+    _lib.check(_lib.load().scmp_permute_code_columns(
+        c.data_ptr(), rows, c.shape[-1], src.data_ptr(), Dp, out.data_ptr(), shape[-1],
+        stream), "scmp_permute_code_columns")
+    return out
+
+
 def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.Epilogue",
             y=None, iout=None, ldy=None, bsy=0, chunk=0, d_class=None, impl=None, tile=None,
             row_map=None):
     """scmp_sc_gemm on the current stream. ca / cb are code buffers (batch, rows_pad, ld)
     or (rows_pad, ld)."""
-    g = _lib.GemmArgs()
-    g.ca, g.lda = ca.data_ptr(), ca.shape[-1]
-    g.bsa = ca.shape[-2] * ca.shape[-1] if ca.dim() == 3 else 0
-    g.cb, g.ldb = cb.data_ptr(), cb.shape[-1]
-    g.bsb = cb.shape[-2] * cb.shape[-1] if cb.dim() == 3 else 0
-    g.N, g.M, g.D, g.batch = N, M, D, batch
-    g.bipolar, g.JP = 1 if tabs.bipolar else 0, tabs.JP
     dev = ca.device
     stream = _lib.stream_of(dev)
     if impl is None:
@@ -170,9 +197,27 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
         if l4 is None and impl == _lib.GEMM_MFMA_FP4:
             raise ValueError("sc_matmul: the stream table has counts FP4 cannot represent")
         impl = _lib.GEMM_MFMA_FP4 if l4 is not None else _lib.GEMM_MFMA
-    g.lut = tabs.lut4(stream).data_ptr() if impl == _lib.GEMM_MFMA_FP4 else tabs.lut.data_ptr()
     dc = d_class if d_class is not None else tabs.d_class
+    gcls = None
+    if impl == _lib.GEMM_MFMA_FP4 and d_class is None and not 0 < chunk < D:
+        runs = _fp4_class_runs(tabs, D)
+        if runs is not None:
+            # every class's inner dimensions side by side (an exact integer sum in any
+            # order), so the kernel holds one class table in LDS at a time
+            src, gcls, D = runs
+            ca = _permute_codes(ca, src, D, stream)
+            cb = _permute_codes(cb, src, D, stream)
+            dc = None
+    g = _lib.GemmArgs()
+    g.ca, g.lda = ca.data_ptr(), ca.shape[-1]
+    g.bsa = ca.shape[-2] * ca.shape[-1] if ca.dim() == 3 else 0
+    g.cb, g.ldb = cb.data_ptr(), cb.shape[-1]
+    g.bsb = cb.shape[-2] * cb.shape[-1] if cb.dim() == 3 else 0
+    g.N, g.M, g.D, g.batch = N, M, D, batch
+    g.bipolar, g.JP = 1 if tabs.bipolar else 0, tabs.JP
+    g.lut = tabs.lut4(stream).data_ptr() if impl == _lib.GEMM_MFMA_FP4 else tabs.lut.data_ptr()
     g.d_class = _lib.ptr(dc)
+    g.group_class = _lib.ptr(gcls)
     g.nclass = tabs.nclass
     g.chunk = chunk
     g.epi = epi
@@ -191,7 +236,7 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         g.workspace, g.workspace_bytes = ws.data_ptr(), nbytes
     _lib.check(lib.scmp_sc_gemm(g, stream), "scmp_sc_gemm")
-    return ws  # keep the workspace alive until the stream has consumed it
+    return ws, ca, cb  # keep the buffers alive until the stream has consumed them
 
 
 def _codes(rows: int, D: int, device, batch: int = 0) -> torch.Tensor:

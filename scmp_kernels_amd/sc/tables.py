@@ -115,6 +115,28 @@ class StreamTables:
     _bitlut: Optional[torch.Tensor] = None
     _lut4: Optional[torch.Tensor] = None
     _fp4_ok: Optional[bool] = None
+    _runs: Optional[tuple] = None
+
+    def class_runs(self):
+        """The inner dimensions laid out in runs of one class, each run padded to whole
+        groups of 8: (src, group_class, Dp) with src[p] the d at position p (-1: padding),
+        an int32 device tensor of Dp entries, and group_class the class of each group of 8
+        positions (Dp / 8 entries). Built on first use."""
+        if self._runs is None:
+            cls = self.class_of.astype(np.int64)
+            counts = np.bincount(cls, minlength=self.nclass)
+            padded = (counts + 7) // 8 * 8
+            start = np.concatenate([[0], np.cumsum(padded)[:-1]])     # run start per class
+            first = np.concatenate([[0], np.cumsum(counts)[:-1]])     # in the sorted order
+            order = np.argsort(cls, kind="stable")
+            pos = start[cls[order]] + (np.arange(len(order)) - first[cls[order]])
+            Dp = int(padded.sum())
+            src = np.full(Dp, -1, dtype=np.int32)
+            src[pos] = order
+            gcls = np.repeat(np.arange(self.nclass, dtype=np.int32), padded // 8)
+            dev = self.lut.device
+            self._runs = (torch.from_numpy(src).to(dev), torch.from_numpy(gcls).to(dev), Dp)
+        return self._runs
 
     def lut4(self, stream) -> Optional[torch.Tensor]:
         """FP4 (e2m1) form of the table, or None when some count is not representable

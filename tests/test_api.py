@@ -175,3 +175,59 @@ def test_empty_operands_give_empty_output(gran, sa, sb, out):
 def test_zero_inner_dimension_rejected():
     with pytest.raises(ValueError, match="inner dimension"):
         sc_matmul(torch.zeros(4, 0), torch.zeros(5, 0))
+
+
+def _fake_tables(class_of, JP=64):
+    from types import SimpleNamespace
+    from scmp_kernels_amd.sc import tables as TB
+    class_of = np.asarray(class_of, dtype=np.int32)
+    t = SimpleNamespace(class_of=class_of, nclass=int(class_of.max()) + 1, JP=JP,
+                        D=len(class_of), lut=torch.zeros(1), _runs=None)
+    t.class_runs = lambda: TB.StreamTables.class_runs(t)
+    return t
+
+
+@pytest.mark.parametrize("D,nclass,seed", [(4096, 64, 0), (777, 64, 1), (100, 7, 2),
+                                           (64, 1, 3), (513, 300, 4)])
+def test_class_runs_layout(D, nclass, seed):
+    """Every d appears once, in runs of its own class (increasing d inside a run), each
+    run padded with -1 to whole groups of 8 whose class is the run's."""
+    rng = np.random.default_rng(seed)
+    class_of = rng.integers(0, nclass, D)
+    class_of[:nclass] = np.arange(nclass)                  # every class occurs
+    t = _fake_tables(class_of)
+    src, gcls, Dp = t.class_runs()
+    src, gcls = src.numpy(), gcls.numpy()
+    assert Dp % 8 == 0 and len(src) == Dp and len(gcls) == Dp // 8
+    assert sorted(src[src >= 0].tolist()) == list(range(D))
+    counts = np.bincount(class_of, minlength=t.nclass)
+    assert Dp == int(((counts + 7) // 8 * 8).sum())
+    grp = np.repeat(gcls, 8)
+    real = src >= 0
+    np.testing.assert_array_equal(class_of[src[real]], grp[real])
+    for c in range(t.nclass):
+        pos = np.nonzero(grp == c)[0]
+        if len(pos):
+            assert pos[-1] - pos[0] + 1 == len(pos)            # one contiguous run
+            run = src[pos]
+            k = counts[c]
+            assert (run[:k] >= 0).all() and (run[k:] == -1).all()
+            assert (np.diff(run[:k]) > 0).all()
+
+
+def test_class_runs_selection(monkeypatch):
+    from scmp_kernels_amd.sc import kernels as K
+    monkeypatch.delenv("SCMP_FP4_RUNS", raising=False)
+    assert K._fp4_class_runs(_fake_tables(np.zeros(512, int)), 512) is None   # one class
+    # 8 classes of 64-interval tables fit in LDS: all of them are staged, no runs
+    assert K._fp4_class_runs(_fake_tables(np.arange(512) % 8), 512) is None
+    # 64 classes do not fit: runs when the padding is small
+    t = _fake_tables(np.arange(4096) % 64)
+    src, gcls, Dp = K._fp4_class_runs(t, 4096)
+    assert Dp == 4096
+    # ... but not when the runs would grow D by more than an eighth
+    assert K._fp4_class_runs(_fake_tables(np.arange(256) % 64), 256) is None
+    monkeypatch.setenv("SCMP_FP4_RUNS", "1")
+    assert K._fp4_class_runs(_fake_tables(np.arange(256) % 64), 256)[2] == 512
+    monkeypatch.setenv("SCMP_FP4_RUNS", "0")
+    assert K._fp4_class_runs(t, 4096) is None

@@ -482,3 +482,112 @@ def test_per_row_3d_vs_oracle():
     b = rng.standard_normal((5, 33, 64)).astype(np.float32)
     bits_equal(sc_matmul(T(a), T(b), "per_row"), O.sc_matmul(a, b, "per_row"))
     bits_equal(sc_matmul(T(a), T(b), "per_tensor"), O.sc_matmul(a, b, "per_tensor"))
+
+
+# -------------------------------------------------------------------------------------
+# per-d table classes in runs: both code buffers' columns rearranged class by class, one
+# class table in LDS at a time (SCMP_FP4_RUNS=1 forces the layout where the padding rule
+# would not choose it)
+# -------------------------------------------------------------------------------------
+
+RUNS_CASES = [
+    # (N, M, D, L, R, bipolar)
+    (257, 300, 777, 64, 64, False),      # split tiles, runs padded to whole groups
+    (260, 270, 600, 128, 128, True),
+    (70, 45, 96, 32, 32, True),
+    (40, 31, 50, 16, 16, False),         # 16-interval tables (four d per k-step)
+    (300, 200, 2048, 64, 64, True),
+    (33, 97, 77, 64, 64, False),         # fewer d than classes
+]
+
+
+def _nclass(L, R, bipolar, D):
+    from scmp_kernels_amd.sc import kernels as K
+    return K._get_tables(None, 8, L, R, bipolar, D, _dev()).nclass
+
+
+@pytest.mark.parametrize("case", RUNS_CASES)
+def test_gemm_class_runs(case, monkeypatch):
+    N, M, D, L, R, bip = case
+    monkeypatch.setenv("SCMP_FP4_RUNS", "1")
+    assert _nclass(L, R, bip, D) > 1
+    rng = np.random.default_rng(N * 5 + M + D)
+    a = rng.standard_normal((N, D)).astype(np.float32)
+    b = rng.standard_normal((M, D)).astype(np.float32)
+    a[1] = 0.0
+    got = _int_accum_gpu(a, b, L=L, R=R, bipolar=bip, impl=2)
+    np.testing.assert_array_equal(got, _int_accum_ref(a, b, L=L, R=R, bipolar=bip))
+
+
+@pytest.mark.parametrize("kw,shape", [
+    (dict(mode="unipolar", group_a=4, group_b=4, stoc_len=64, rng_levels=64), (300, 200, 1024)),
+    (dict(mode="bipolar", stoc_len=64, rng_levels=64), (129, 260, 2048)),
+])
+def test_sc_matmul_class_runs_chosen(kw, shape, monkeypatch):
+    """Shapes where the run layout is chosen by itself (64 classes of 64-interval tables,
+    D a multiple of 512: no padding), against the oracle."""
+    from scmp_kernels_amd import sc_matmul
+    from scmp_kernels_amd.sc import kernels as K
+    monkeypatch.delenv("SCMP_FP4_RUNS", raising=False)
+    N, M, D = shape
+    tabs = K._get_tables(None, 8, 64, 64, kw["mode"] == "bipolar", D, _dev())
+    assert K._fp4_class_runs(tabs, D) is not None
+    rng = np.random.default_rng(N + 2 * M + D)
+    a = rng.standard_normal((N, D)).astype(np.float32)
+    b = (rng.standard_normal((M, D)) * 0.05).astype(np.float32)
+    bits_equal(sc_matmul(T(a), T(b), "per_row", **kw), O.sc_matmul(a, b, "per_row", **kw))
+
+
+def test_class_runs_equal_global_tables_full_size(monkeypatch):
+    """cfg5's L=64 level shape (1365 x 4096 x 4096, unipolar, groups of 4): the run layout
+    and the per-d global-table path give the same bits."""
+    from scmp_kernels_amd import sc_matmul
+    dev = _dev()
+    g = torch.Generator(device=dev).manual_seed(5)
+    a = torch.randn((1365, 4096), device=dev, generator=g)
+    b = torch.randn((4096, 4096), device=dev, generator=g) * 0.02
+    kw = dict(mode="unipolar", group_a=4, group_b=4, stoc_len=64, rng_levels=64)
+    monkeypatch.setenv("SCMP_FP4_RUNS", "0")
+    ref = sc_matmul(a, b, "per_row", **kw)
+    monkeypatch.delenv("SCMP_FP4_RUNS")
+    got = sc_matmul(a, b, "per_row", **kw)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32),
+                                  ref.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [(6, 197, 64, 197), (3, 300, 136, 33)])
+def test_per_head_class_runs_vs_oracle(shape, monkeypatch):
+    """Batched codes (one buffer per head) through the run layout."""
+    from scmp_kernels_amd import sc_matmul
+    monkeypatch.setenv("SCMP_FP4_RUNS", "1")
+    BH, N, D, M = shape
+    rng = np.random.default_rng(sum(shape) + 1)
+    q = rng.standard_normal((BH, N, D)).astype(np.float32)
+    k = rng.standard_normal((BH, M, D)).astype(np.float32)
+    kw = dict(stoc_len=64, rng_levels=64)
+    bits_equal(sc_matmul(T(q), T(k), "per_head", **kw), O.sc_matmul(q, k, "per_head", **kw))
+
+
+@pytest.mark.parametrize("rows,ld_in,ncols,ld_out", [(7, 4096, 4096, 4096), (1, 48, 40, 48),
+                                                     (300, 20000, 19999, 20000),
+                                                     (9, 100, 117, 128), (513, 16384, 16000,
+                                                                          16016)])
+def test_permute_code_columns(rows, ld_in, ncols, ld_out):
+    """scmp_permute_code_columns against numpy: gathered columns, -1 entries and the columns
+    past ncols zero (the three launch forms: 4 rows or 1 row per workgroup through LDS, and
+    a row stride that is not a multiple of 16)."""
+    from scmp_kernels_amd import _lib
+    dev = _dev()
+    rng = np.random.default_rng(rows + ld_in)
+    x = rng.integers(0, 256, (rows, ld_in), dtype=np.uint8)
+    src = rng.integers(0, ld_in, ncols).astype(np.int32)
+    src[rng.random(ncols) < 0.1] = -1
+    xin, s = T(x), torch.from_numpy(src).to(dev)
+    out = torch.full((rows, ld_out), 0xAB, dtype=torch.uint8, device=dev)
+    _lib.check(_lib.load().scmp_permute_code_columns(
+        xin.data_ptr(), rows, ld_in, s.data_ptr(), ncols, out.data_ptr(), ld_out,
+        _lib.stream_of(dev)), "scmp_permute_code_columns")
+    ref = np.zeros((rows, ld_out), np.uint8)
+    ref[:, :ncols] = np.where(src >= 0, x[:, np.clip(src, 0, None)], 0)
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
