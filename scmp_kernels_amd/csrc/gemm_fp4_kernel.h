@@ -68,8 +68,10 @@ struct Fp4Geom {
     static constexpr int SPD = KS / KSU;
     static constexpr int DPU = JPF == 16 ? 4 : JPF == 32 ? 2 : 1;    // d per unit (<= 1 k-step)
     static constexpr int UPG = JPF <= 32 ? 8 / DPU : 8 * SPD;        // units per 8 codes
-    // odd number of 16-byte chunks between LDS rows: spreads rows over the bank groups
-    static constexpr int LS = 16 * ((ROWB / 16) | 1);
+    // odd number of 16-byte chunks between LDS rows: spreads rows over the bank groups;
+    // JPF = 16 keeps only the 8 bytes of its 16 intervals, 8 bytes apart (every bank pair
+    // holds rows, where a 16-byte stride would leave half the banks unread)
+    static constexpr int LS = JPF == 16 ? 8 : 16 * ((ROWB / 16) | 1);
     static constexpr int TAB = 256 * LS;                          // one table in LDS
 };
 
@@ -100,6 +102,24 @@ __device__ __forceinline__ int fp4_tables_bytes(const GemmP &P) {
                                                                      : 0));
 }
 
+// Copies `rows` stored table rows (ROWB bytes apart) into LDS rows LS bytes apart.
+template <int JPF>
+__device__ __forceinline__ void fp4_copy_rows(uint8_t *dst, const uint8_t *src, int rows, int tid,
+                                              int nt) {
+    using G = Fp4Geom<JPF>;
+    if constexpr (JPF == 16) {
+        for (int r = tid; r < rows; r += nt)
+            *(uint2 *)(dst + r * G::LS) = *(const uint2 *)(src + (int64_t)r * G::ROWB);
+    } else {
+        constexpr int CH = G::ROWB / 16;         // 16-byte chunks per row
+        const v4i *s = (const v4i *)src;
+        for (int e = tid; e < rows * CH; e += nt) {
+            const int row = e / CH, col = e - row * CH;
+            *(v4i *)(dst + row * G::LS + 16 * col) = s[e];
+        }
+    }
+}
+
 // Prologue: the thermometer table T[code][j'] = sign(code) if j' < j(code) else 0 (rows =
 // THERMO code byte: bipolar sign bit | j, unipolar j), and the stream table(s) copied in
 // (LUT_RUNS: by the accumulation loop, per run).
@@ -107,10 +127,11 @@ template <int JPF, int LUTSRC, int NT>
 __device__ __forceinline__ void fp4_load_tables(const GemmP &P, uint8_t *sA, uint8_t *sB) {
     using G = Fp4Geom<JPF>;
     constexpr int U = G::ROWB / 4;             // dwords per stored row (8 intervals each)
+    constexpr int UL = G::LS / 4 < U ? G::LS / 4 : U;   // of them kept in LDS
     const int Ut = P.JP < 8 * U ? P.JP / 8 : U; // dwords holding intervals (JP = 16: 2)
     const int tid = threadIdx.x;
-    for (int e = tid; e < 256 * U; e += NT) {
-        const int row = e / U, u = e - row * U;
+    for (int e = tid; e < 256 * UL; e += NT) {
+        const int row = e / UL, u = e - row * UL;
         const int j = P.bipolar ? (row & 0x7f) : row;
         const uint32_t one = (P.bipolar && (row & 0x80)) ? 0xAu : 0x2u;
         uint32_t w = 0;
@@ -121,15 +142,9 @@ __device__ __forceinline__ void fp4_load_tables(const GemmP &P, uint8_t *sA, uin
         }
         *(uint32_t *)(sA + row * G::LS + 4 * u) = w;
     }
-    if (LUTSRC == LUT_LDS || LUTSRC == LUT_LDS_CLASSES) {
-        constexpr int CH = G::ROWB / 16;         // 16-byte chunks per row
-        const int rows = (LUTSRC == LUT_LDS_CLASSES ? P.nclass : 1) * 256;
-        const v4i *src = (const v4i *)P.lut;
-        for (int e = tid; e < rows * CH; e += NT) {
-            const int row = e / CH, col = e - row * CH;
-            *(v4i *)(sB + row * G::LS + 16 * col) = src[e];
-        }
-    }
+    if (LUTSRC == LUT_LDS || LUTSRC == LUT_LDS_CLASSES)
+        fp4_copy_rows<JPF>(sB, (const uint8_t *)P.lut,
+                           (LUTSRC == LUT_LDS_CLASSES ? P.nclass : 1) * 256, tid, NT);
 }
 
 // acc += the products of inner-dimension groups [g0, g1) (8 d per group) for the operand
@@ -211,16 +226,31 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         const uint32_t w = dl < 4 ? (m ? q[j].z : q[j].x) : (m ? q[j].w : q[j].y);
         return (int)((w >> (8 * (dl & 3))) & 0xffu);
     };
+    // JPF <= 32: the lane half h selects which code bytes of a word it takes. Rotating the
+    // word right by `rot` bits (8h or 16h) moves them to fixed byte positions, so a lookup
+    // costs a constant-position byte extract instead of a variable shift; word w of row i
+    // (w = 0, 1: the group's d 0-3, 4-7), byte t after the rotation.
+    const uint32_t rot = (JPF == 16 ? 16u : 8u) * (uint32_t)h;
+    auto rbyte = [&](uint32_t w, int t) __attribute__((always_inline)) {
+        return (int)((__builtin_amdgcn_alignbit(w, w, rot) >> (8 * t)) & 0xffu);
+    };
+    auto rcode_a = [&](const uint2 (&c)[BA], int i, int w, int t) __attribute__((always_inline)) {
+        return rbyte(w ? c[i].y : c[i].x, t);
+    };
+    auto rcode_b = [&](const uint4 (&q)[BB], int m, int j, int w, int t)
+        __attribute__((always_inline)) {
+        return rbyte(w ? (m ? q[j].w : q[j].y) : (m ? q[j].z : q[j].x), t);
+    };
 
     // JPF = 16: the lane half's two inner dimensions dl, dl + 1 of a unit, 8 bytes (16
     // intervals) of a table row each, side by side in one fragment
     auto stage16 = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&ca)[BA], int cls8,
                        const uint4 (&qb)[BB], int m, int unit) __attribute__((always_inline)) {
-        const int dl = 4 * unit + 2 * h;
+        // d 4 unit + 2h and + 1: bytes 0 and 1 of word `unit` rotated by 16h
 #pragma unroll
         for (int i = 0; i < BA; ++i) {
-            const uint2 r0 = *(const uint2 *)(sA + code_a(ca, i, dl) * LS);
-            const uint2 r1 = *(const uint2 *)(sA + code_a(ca, i, dl + 1) * LS);
+            const uint2 r0 = *(const uint2 *)(sA + rcode_a(ca, i, unit, 0) * LS);
+            const uint2 r1 = *(const uint2 *)(sA + rcode_a(ca, i, unit, 1) * LS);
             F.a[i][0] = (v4i){(int)r0.x, (int)r0.y, (int)r1.x, (int)r1.y};
         }
         const uint8_t *base0 = sB, *base1 = sB;
@@ -236,8 +266,8 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         constexpr int RS = LUTSRC == LUT_GLOBAL ? ROWB : LS;
 #pragma unroll
         for (int j = 0; j < BB; ++j) {
-            const uint2 r0 = *(const uint2 *)(base0 + code_b(qb, m, j, dl) * RS);
-            const uint2 r1 = *(const uint2 *)(base1 + code_b(qb, m, j, dl + 1) * RS);
+            const uint2 r0 = *(const uint2 *)(base0 + rcode_b(qb, m, j, unit, 0) * RS);
+            const uint2 r1 = *(const uint2 *)(base1 + rcode_b(qb, m, j, unit, 1) * RS);
             F.b[j][0] = (v4i){(int)r0.x, (int)r0.y, (int)r1.x, (int)r1.y};
         }
     };
@@ -251,9 +281,12 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         }
         const int dl = JPF == 32 ? 2 * unit + h : unit / SPD;    // d within the group
         const int koff = (JPF == 32 ? 0 : 16 * h) + 32 * KSU * (unit % SPD);
+        // JPF = 32: d 2 unit + h is byte 2 (unit & 1) of word unit / 2 rotated by 8h
+        const int w32 = unit >> 1, t32 = 2 * (unit & 1);
 #pragma unroll
         for (int i = 0; i < BA; ++i) {
-            const uint8_t *p = sA + code_a(ca, i, dl) * LS + koff;
+            const int code = JPF == 32 ? rcode_a(ca, i, w32, t32) : code_a(ca, i, dl);
+            const uint8_t *p = sA + code * LS + koff;
 #pragma unroll
             for (int t = 0; t < KSU; ++t) F.a[i][t] = *(const v4i *)(p + 32 * t);
         }
@@ -271,8 +304,8 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         }
 #pragma unroll
         for (int j = 0; j < BB; ++j) {
-            const uint8_t *p = base + code_b(qb, m, j, dl) * (LUTSRC == LUT_GLOBAL ? ROWB : LS) +
-                               koff;
+            const int code = JPF == 32 ? rcode_b(qb, m, j, w32, t32) : code_b(qb, m, j, dl);
+            const uint8_t *p = base + code * (LUTSRC == LUT_GLOBAL ? ROWB : LS) + koff;
 #pragma unroll
             for (int t = 0; t < KSU; ++t) F.b[j][t] = *(const v4i *)(p + 32 * t);
         }
@@ -296,14 +329,9 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     // wave reaches the same barriers
     auto run_table = [&](int c) __attribute__((always_inline)) {
         c = c < 0 ? 0 : c >= P.nclass ? P.nclass - 1 : c;
-        constexpr int CH = ROWB / 16;
-        const v4i *src = (const v4i *)(glut + (int64_t)c * 256 * ROWB);
-        uint8_t *dst = (uint8_t *)sB;
         __syncthreads();
-        for (int e = (int)threadIdx.x; e < 256 * CH; e += (int)blockDim.x) {
-            const int row = e / CH, col = e - row * CH;
-            *(v4i *)(dst + row * LS + 16 * col) = src[e];
-        }
+        fp4_copy_rows<JPF>((uint8_t *)sB, glut + (int64_t)c * 256 * ROWB, 256,
+                           (int)threadIdx.x, (int)blockDim.x);
         __syncthreads();
     };
 
@@ -506,10 +534,11 @@ sc_gemm_fp4_kernel(GemmP P) {
         int lt = lane;
         asm volatile("" : "+v"(lt));
         const int ecol = lt & 31, ehalf = lt >> 5;
-        // partial-sum slot layout: block (i, c) of this wave, then lane, then the 16
-        // accumulator registers of the lane (the MFMA layout itself, 64 B per lane)
-        auto pblk = [&](int i, int c) __attribute__((always_inline)) {
-            return (int64_t)((wave * BA + i) * BB + c) * 1024 + lt * 16;
+        // partial-sum slot layout: block (i, c) of this wave, then the quarter q of the
+        // lane's 16 accumulator registers, then lane (4 floats each): one 16-byte access per
+        // lane covers 1 KB of consecutive memory
+        auto pofs = [&](int i, int c, int q) __attribute__((always_inline)) {
+            return (int64_t)((wave * BA + i) * BB + c) * 1024 + q * 256 + lt * 4;
         };
 
         const bool shared = g0 != 0 || g1 != ngroups;
@@ -528,11 +557,11 @@ sc_gemm_fp4_kernel(GemmP P) {
             for (int i = 0; i < BA; ++i)
 #pragma unroll
                 for (int c = 0; c < BB; ++c) {
-                    v4f *dst = (v4f *)(mine + pblk(i, c));
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
-                        dst[q] = (v4f){acc[i][c][4 * q], acc[i][c][4 * q + 1],
-                                       acc[i][c][4 * q + 2], acc[i][c][4 * q + 3]};
+                        *(v4f *)(mine + pofs(i, c, q)) =
+                            (v4f){acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2],
+                                  acc[i][c][4 * q + 3]};
                 }
             // The barrier waits for every wave's stores; one device-scope fence then
             // publishes them (and, for the finisher, makes the others' visible: the L1
@@ -566,7 +595,7 @@ sc_gemm_fp4_kernel(GemmP P) {
 #pragma unroll
                             for (int q = 0; q < 4; ++q)
                                 ov[c][q] = __builtin_nontemporal_load(
-                                    (const v4f *)(other + pblk(i, c)) + q);
+                                    (const v4f *)(other + pofs(i, c, q)));
 #pragma unroll
                         for (int c = 0; c < BB; ++c)
 #pragma unroll

@@ -161,7 +161,7 @@ def _fp4_class_runs(tabs: "_tables.StreamTables", D: int):
     if env == "0" or tabs.nclass <= 1 or D != tabs.D:
         return None
     rowb = max(tabs.JP, 32) // 2
-    tab = 256 * 16 * ((rowb // 16) | 1)          # one table in LDS (padded rows)
+    tab = 256 * (8 if tabs.JP == 16 else 16 * ((rowb // 16) | 1))   # one table in LDS
     if env != "1" and tab * (1 + tabs.nclass) + _FP4_STAGE_BYTES <= _FP4_MAX_LDS:
         return None                              # every class table fits in LDS
     runs = tabs.class_runs()
