@@ -831,10 +831,16 @@ static void launch_group_pt(const scmp_quant_args &a, dim3 grid, int G, int cpr,
 
 // A group too large for 256 threads' registers takes 1024 threads (multiply-by-reciprocal
 // variants: the per-head attention operands, one group per head), so it is read once.
+// `wide`: few groups of 1025 to 4096 chunks (a row subset of a mixed-precision level)
+// also take 1024 threads, four times the loads in flight per group.
 template <int OP>
 static void launch_group(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt,
-                         bool vec, hipStream_t stream) {
-    if (npt <= 4) {
+                         bool vec, bool wide, hipStream_t stream) {
+    if (wide) {
+        launch_group_pt<OP, 4, kBigGroupThreads>(a, grid, G, cpr,
+                                                 (int)cdiv((int64_t)G * cpr, kBigGroupThreads),
+                                                 vec, stream);
+    } else if (npt <= 4) {
         launch_group_pt<OP, 4>(a, grid, G, cpr, npt, vec, stream);
     } else if (npt <= kMaxChunks || OP != QOP_MUL) {
         launch_group_pt<OP, kMaxChunks>(a, grid, G, cpr, npt, vec, stream);
@@ -846,9 +852,28 @@ static void launch_group(const scmp_quant_args &a, dim3 grid, int G, int cpr, in
     }
 }
 
+// Compute units of the current device (cached per device).
+static int quant_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stream) {
     const int64_t ngroups = cdiv(a.rows, G);
     const int64_t cpr = cdiv(a.cols, 4);
+    // fewer than two 256-thread workgroups per compute unit, each group one to four chunks
+    // per thread at 1024 threads
+    const bool wide = ngroups < 2 * (int64_t)quant_cu_count() && G * cpr > kBigGroupThreads &&
+                      G * cpr <= 4 * (int64_t)kBigGroupThreads;
     const int64_t per = cdiv(G * cpr, kGroupThreads);
     const bool vec = (a.ld % 4 == 0) && (((uintptr_t)a.x & 15) == 0) &&
                      (a.smooth_mode == SCMP_SMOOTH_NONE || ((uintptr_t)a.smooth & 15) == 0);
@@ -856,13 +881,13 @@ static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stre
     const int npt = (int)(per <= kMaxChunks ? per : kMaxChunks + 1);   // at 256 threads
     switch (a.variant) {
     case SCMP_Q_GROUP_SYM:
-        launch_group<QOP_DIV>(a, grid, (int)G, (int)cpr, npt, vec, stream);
+        launch_group<QOP_DIV>(a, grid, (int)G, (int)cpr, npt, vec, wide, stream);
         break;
     case SCMP_Q_GROUP_ASYM:
-        launch_group<QOP_DIVZP>(a, grid, (int)G, (int)cpr, npt, vec, stream);
+        launch_group<QOP_DIVZP>(a, grid, (int)G, (int)cpr, npt, vec, wide, stream);
         break;
     default:
-        launch_group<QOP_MUL>(a, grid, (int)G, (int)cpr, npt, vec, stream);
+        launch_group<QOP_MUL>(a, grid, (int)G, (int)cpr, npt, vec, wide, stream);
         break;
     }
     SCMP_LAUNCH_CHECK("scmp_quantize/group");   // the kernel zeroes the padding rows too

@@ -189,6 +189,23 @@ def test_quant_grouped(G):
     bits_equal(s, rs); bits_equal(zp, rzp); bits_equal(xi, rxi)
 
 
+@pytest.mark.parametrize("rows,cols,G", [(301, 4096, 4), (97, 3000, 4), (50, 2100, 2),
+                                         (9, 1030, 4)])
+def test_quant_grouped_wide(rows, cols, G):
+    """Few groups of 1025-4096 four-column chunks: 1024-thread workgroups (a ragged last
+    group, rows not a multiple of 4 columns, one to four chunks per thread)."""
+    from scmp_kernels_amd.quant import _grouped_symmetric_quant, _grouped_asymmetric_quant
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    x[rng.integers(0, rows, 5)] *= 30.0
+    s, xi, sg = _grouped_symmetric_quant(T(x), G, 127)
+    rs, rxi, rsg = O.grouped_sym(x, G, 127)
+    bits_equal(s, rs); bits_equal(xi, rxi); bits_equal(sg, rsg)
+    s, zp, xi = _grouped_asymmetric_quant(T(x), G, 255)
+    rs, rzp, rxi = O.grouped_asym(x, G, 255)
+    bits_equal(s, rs); bits_equal(zp, rzp); bits_equal(xi, rxi)
+
+
 def test_quant_grouped_batched():
     from scmp_kernels_amd.quant import _grouped_symmetric_quant_batched
     rng = np.random.default_rng(4)
