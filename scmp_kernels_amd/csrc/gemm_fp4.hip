@@ -19,10 +19,10 @@ static int device_cu_count() {
     return cached[dev];
 }
 
-// Schedule of the non-chunked FP4 kernel (256 x TC tiles, one workgroup per CU).
+// Schedule of the non-chunked FP4 kernel (TR x TC tiles, one workgroup per CU).
 struct Fp4Plan {
     int64_t tilesA, tilesB, ntiles;
-    int TC;                   // tile columns: 256, or 64 when M <= 64 (narrow tiles)
+    int TR, TC;               // tile rows x columns: 256 x 256, 256 x 64 (narrow), 128 x 512
     int nwg;                  // persistent workgroups
     bool split;               // some tiles are shared by several workgroups
     int64_t cnt_bytes, part_bytes;
@@ -32,12 +32,25 @@ struct Fp4Plan {
 // only when it pays: inner dimension of at least 64 groups (512 d), and at least 32 groups
 // per workgroup. Otherwise every workgroup takes whole tiles. Outputs at most 64 columns
 // wide (attention's P.V per head) use 256 x 64 tiles when the stream table is a single one
-// (narrow_ok), instead of computing three quarters of a 256 x 256 tile on padding.
+// (narrow_ok), instead of computing three quarters of a 256 x 256 tile on padding. 128 x 512
+// tiles are taken when they cover N x M with at least 3% less padded area than 256 x 256
+// (a row count just above a multiple of 256, such as a mixed-precision level's rows).
 static Fp4Plan fp4_plan(int64_t N, int64_t M, int64_t D, int64_t batch, int ncu,
                         bool narrow_ok) {
     Fp4Plan p;
-    p.TC = narrow_ok && M <= 64 ? 64 : 256;
-    p.tilesA = cdiv(N, 256);
+    // tile counts of the two shapes (equal tile areas)
+    const int64_t sq = cdiv(N, 256) * cdiv(M, 256), wide = cdiv(N, 128) * cdiv(M, 512);
+    if (narrow_ok && M <= 64) {
+        p.TR = 256;
+        p.TC = 64;
+    } else if (wide * 100 <= sq * 97) {
+        p.TR = 128;
+        p.TC = 512;
+    } else {
+        p.TR = 256;
+        p.TC = 256;
+    }
+    p.tilesA = cdiv(N, p.TR);
     p.tilesB = cdiv(M, p.TC);
     p.ntiles = p.tilesA * p.tilesB * batch;
     const int64_t G = cdiv(D, 8);
@@ -55,7 +68,7 @@ static Fp4Plan fp4_plan(int64_t N, int64_t M, int64_t D, int64_t batch, int ncu,
     p.nwg = (int)nwg;
     p.split = (W % p.nwg) != 0 || (W / p.nwg) % G != 0;
     p.cnt_bytes = (p.ntiles * 4 + 255) / 256 * 256;
-    p.part_bytes = (int64_t)p.nwg * 2 * (256 * p.TC) * 4;
+    p.part_bytes = (int64_t)p.nwg * 2 * (p.TR * p.TC) * 4;
     return p;
 }
 

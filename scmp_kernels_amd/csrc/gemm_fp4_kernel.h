@@ -36,6 +36,7 @@
 // for one table width each (separate translation units compile in parallel).
 #pragma once
 
+#include <type_traits>
 #include "gemm_common.h"
 
 namespace scmp {
@@ -52,9 +53,16 @@ __device__ __forceinline__ v16f mfma_fp4(v4i a, v4i b, v16f c) {
 // laid out in runs of one class).
 enum { LUT_LDS = 0, LUT_LDS_CLASSES = 1, LUT_GLOBAL = 2, LUT_RUNS = 3 };
 
-// floats of the per-tile epilogue area of a 256 x 256 tile: 3 factors per row and per
-// column, then one int64 output offset per row (two floats' worth each)
-constexpr int kFactorFloats = 6 * 256 + 2 * 256;
+// floats of the per-tile epilogue area: 3 factors per row and per column, then one int64
+// output offset per row (two floats' worth each), for the largest tile shapes: 256 x 256
+// (2048 floats) and 128 x 512 (2176)
+constexpr int kFactorFloats = 5 * 128 + 3 * 512;
+
+// Tile shapes of the persistent kernel (rows of A x rows of B per workgroup, four waves):
+// 256 x 256 (2 x 2 waves of 128 x 128), narrow 256 x 64 (4 x 1 waves of 64 x 64) for outputs
+// at most 64 wide, and wide 128 x 512 (1 x 4 waves of 128 x 128), which pads a row count
+// such as 1365 to 1408 instead of 1536.
+enum { TILE_SQUARE = 0, TILE_NARROW = 1, TILE_WIDE = 2 };
 
 // accelerator complex dies (XCDs) of an MI355X; workgroup i runs on XCD i mod 8
 constexpr int kXcds = 8;
@@ -422,7 +430,7 @@ __device__ __forceinline__ int64_t fp4_slot(int64_t c, int64_t t, int64_t W, int
 // consecutive values of one row. Row factors and output row offsets come from LDS (nrb:
 // the lane's tile-local row of i = r = 0), column factors once per block column (mcb, mb:
 // tile-local and global column of c = 0). Only stores reach global memory.
-template <int KIND, int BA, int BB>
+template <int KIND, int BA, int BB, int TR, int TC>
 __device__ __forceinline__ void fp4_drain(const GemmP &P, const v16f (&acc)[BA][BB],
                                           const float *s_rowf, const float *s_colf,
                                           const int64_t *s_rowo, const EpiUniform &eu,
@@ -433,8 +441,8 @@ __device__ __forceinline__ void fp4_drain(const GemmP &P, const v16f (&acc)[BA][
     for (int c = 0; c < BB; ++c) {
         const int mc = mcb + 32 * c;
         cb[c] = s_colf[mc];
-        cz[c] = s_colf[256 + mc];
-        cs[c] = s_colf[512 + mc];
+        cz[c] = s_colf[TC + mc];
+        cs[c] = s_colf[2 * TC + mc];
         mok[c] = mb + 32 * c < P.M;
     }
     constexpr bool ZP = KIND == SCMP_EPI_ZP_ROWCOL || KIND == SCMP_EPI_ZP_SCALAR;
@@ -450,8 +458,8 @@ __device__ __forceinline__ void fp4_drain(const GemmP &P, const v16f (&acc)[BA][
             const int nr = nrb + 32 * i + 8 * (r >> 2) + (r & 3);
             ro[r] = s_rowo[nr];
             ra[r] = RA ? s_rowf[nr] : 0.f;
-            rz[r] = KIND == SCMP_EPI_ZP_ROWCOL ? s_rowf[256 + nr] : 0.f;
-            rs[r] = ZP ? s_rowf[512 + nr] : 0.f;
+            rz[r] = KIND == SCMP_EPI_ZP_ROWCOL ? s_rowf[TR + nr] : 0.f;
+            rs[r] = ZP ? s_rowf[2 * TR + nr] : 0.f;
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -481,10 +489,10 @@ sc_gemm_fp4_kernel(GemmP P) {
     uint8_t *sA = smem;                                  // thermometer table
     uint8_t *sB = smem + Fp4Geom<JPF>::TAB;              // stream table(s)
     constexpr int TR = WA * BA * 32, TC = WB * BB * 32;   // tile rows / columns
-    static_assert(TR <= 256 && TC <= 256, "epilogue factor area holds 256 rows / columns");
-    float *s_rowf = (float *)(smem + ((tabs + 15) & ~15)); // [3][256] sa, za, suma
-    float *s_colf = s_rowf + 3 * 256;                    // [3][256] sb, zb, sumb
-    int64_t *s_rowo = (int64_t *)(s_colf + 3 * 256);     // [256] output row offsets
+    static_assert(5 * TR + 3 * TC <= kFactorFloats, "epilogue factor area too small");
+    float *s_rowf = (float *)(smem + ((tabs + 15) & ~15)); // [3][TR] sa, za, suma
+    float *s_colf = s_rowf + 3 * TR;                     // [3][TC] sb, zb, sumb
+    int64_t *s_rowo = (int64_t *)(s_colf + 3 * TC);      // [TR] output row offsets
 
     fp4_load_tables<JPF, LUTSRC, NT>(P, sA, sB);
     __syncthreads();
@@ -622,15 +630,15 @@ sc_gemm_fp4_kernel(GemmP P) {
                     float f[3] = {0.f, 0.f, 0.f};
                     if (tr0 + e < P.N) epi_row_factors(P.epi, tr0 + e, batch, f);
                     s_rowf[e] = f[0];
-                    s_rowf[256 + e] = f[1];
-                    s_rowf[512 + e] = f[2];
+                    s_rowf[TR + e] = f[1];
+                    s_rowf[2 * TR + e] = f[2];
                 }
                 for (int e = tid; e < TC; e += NT) {
                     float f[3] = {0.f, 0.f, 0.f};
                     if (tc0 + e < P.M) epi_col_factors(P.epi, tc0 + e, batch, f);
                     s_colf[e] = f[0];
-                    s_colf[256 + e] = f[1];
-                    s_colf[512 + e] = f[2];
+                    s_colf[TC + e] = f[1];
+                    s_colf[2 * TC + e] = f[2];
                 }
             }
             const EpiUniform eu = fp32 ? epi_uniform(P.epi, batch) : EpiUniform{0.f, 0.f, 0.f, 0.f};
@@ -641,23 +649,23 @@ sc_gemm_fp4_kernel(GemmP P) {
             const int64_t ybase = batch * P.bsy;
             switch (P.epi.kind) {
             case SCMP_EPI_INT:
-                fp4_drain<SCMP_EPI_INT>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                fp4_drain<SCMP_EPI_INT, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
                 break;
             case SCMP_EPI_ROWCOL:
-                fp4_drain<SCMP_EPI_ROWCOL>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                fp4_drain<SCMP_EPI_ROWCOL, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
                 break;
             case SCMP_EPI_SCALAR:
-                fp4_drain<SCMP_EPI_SCALAR>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                fp4_drain<SCMP_EPI_SCALAR, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
                 break;
             case SCMP_EPI_HEAD:
-                fp4_drain<SCMP_EPI_HEAD>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                fp4_drain<SCMP_EPI_HEAD, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
                 break;
             case SCMP_EPI_ZP_ROWCOL:
-                fp4_drain<SCMP_EPI_ZP_ROWCOL>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb,
+                fp4_drain<SCMP_EPI_ZP_ROWCOL, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb,
                                               ybase);
                 break;
             default:
-                fp4_drain<SCMP_EPI_ZP_SCALAR>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb,
+                fp4_drain<SCMP_EPI_ZP_SCALAR, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb,
                                               ybase);
                 break;
             }
@@ -808,14 +816,15 @@ static size_t fp4_tables_bytes_host(const GemmP &P) {
                                                                              : 0));
 }
 
-// Non-chunked: 256 x 256 tiles, each wave 128 x 128 (4 x 4 blocks of 32 x 32), or narrow
-// 256 x 64 tiles, each wave 64 x 64 (2 x 2 blocks); MFMA / LDS-read interleaving enforced,
-// epilogue fused; P.nwg persistent workgroups (P.ntiles when no split workspace was given:
-// one tile each, no partial sums).
-template <int JPF, int LUTSRC, bool NARROW = false>
+// Non-chunked, tile shape SHAPE (waves of 4 x 4 blocks of 32 x 32, narrow: 2 x 2);
+// MFMA / LDS-read interleaving enforced, epilogue fused; P.nwg persistent workgroups
+// (P.ntiles when no split workspace was given: one tile each, no partial sums).
+template <int JPF, int LUTSRC, int SHAPE = TILE_SQUARE>
 static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
-    constexpr int BA = NARROW ? 2 : 4, BB = NARROW ? 2 : 4, WA = NARROW ? 4 : 2,
-                  WB = NARROW ? 1 : 2;
+    constexpr bool NARROW = SHAPE == TILE_NARROW;
+    constexpr int BA = NARROW ? 2 : 4, BB = NARROW ? 2 : 4,
+                  WA = NARROW ? 4 : SHAPE == TILE_WIDE ? 1 : 2,
+                  WB = NARROW ? 1 : SHAPE == TILE_WIDE ? 4 : 2;
     GemmP P = P0;
     auto kern = sc_gemm_fp4_kernel<JPF, BA, BB, WA, WB, LUTSRC, true>;
     const size_t lds = ((fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15) +
@@ -859,6 +868,16 @@ int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t
             return SCMP_E_ARG;
         }
     }
+    // the non-chunked kernel in the planned tile shape (narrow: single table only)
+    auto main_kernel = [&](auto src) {
+        constexpr int SRC = decltype(src)::value;
+        return P.tile_cols == 512 ? launch_fp4_main<JPF, SRC, TILE_WIDE>(P, batch, s)
+                                  : launch_fp4_main<JPF, SRC>(P, batch, s);
+    };
+    using Lds = std::integral_constant<int, LUT_LDS>;
+    using Classes = std::integral_constant<int, LUT_LDS_CLASSES>;
+    using Global = std::integral_constant<int, LUT_GLOBAL>;
+    using Runs = std::integral_constant<int, LUT_RUNS>;
     const int64_t stage = kFactorFloats * (int64_t)sizeof(float);
     if (P.group_class != nullptr) {
         if (chunked || P.d_class != nullptr || P.nclass <= 0) {
@@ -866,25 +885,21 @@ int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t
                       "and nclass > 0");
             return SCMP_E_ARG;
         }
-        return launch_fp4_main<JPF, LUT_RUNS>(P, batch, s);
+        return main_kernel(Runs{});
     }
     if (P.d_class == nullptr) {
         if constexpr (JPF != 16)
             if (chunked) return launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s);
-        return P.tile_cols == 64 ? launch_fp4_main<JPF, LUT_LDS, true>(P, batch, s)
-                                 : launch_fp4_main<JPF, LUT_LDS>(P, batch, s);
+        return P.tile_cols == 64 ? launch_fp4_main<JPF, LUT_LDS, TILE_NARROW>(P, batch, s)
+                                 : main_kernel(Lds{});
     }
-    if constexpr (JPF == 16) {
-        if (P.nclass > 0 && (int64_t)G::TAB * (1 + P.nclass) + stage <= kFp4MaxLds)
-            return launch_fp4_main<JPF, LUT_LDS_CLASSES>(P, batch, s);
-        return launch_fp4_main<JPF, LUT_GLOBAL>(P, batch, s);
-    } else {
-        if (P.nclass > 0 && (int64_t)G::TAB * (1 + P.nclass) + stage <= kFp4MaxLds)
-            return chunked ? launch_fp4_chunked<JPF, LUT_LDS_CLASSES>(P, batch, s)
-                           : launch_fp4_main<JPF, LUT_LDS_CLASSES>(P, batch, s);
-        return chunked ? launch_fp4_chunked<JPF, LUT_GLOBAL>(P, batch, s)
-                       : launch_fp4_main<JPF, LUT_GLOBAL>(P, batch, s);
+    const bool fits = P.nclass > 0 && (int64_t)G::TAB * (1 + P.nclass) + stage <= kFp4MaxLds;
+    if constexpr (JPF != 16) {
+        if (chunked)
+            return fits ? launch_fp4_chunked<JPF, LUT_LDS_CLASSES>(P, batch, s)
+                        : launch_fp4_chunked<JPF, LUT_GLOBAL>(P, batch, s);
     }
+    return fits ? main_kernel(Classes{}) : main_kernel(Global{});
 }
 
 }  // namespace scmp

@@ -149,7 +149,7 @@ def _gemm_impl() -> Optional[int]:
 
 # LDS of one FP4 GEMM workgroup (gemm_fp4_kernel.h: kFp4MaxLds, kFactorFloats)
 _FP4_MAX_LDS = 160 * 1024
-_FP4_STAGE_BYTES = (6 * 256 + 2 * 256) * 4
+_FP4_STAGE_BYTES = (5 * 128 + 3 * 512) * 4
 
 
 def _fp4_class_runs(tabs: "_tables.StreamTables", D: int):
