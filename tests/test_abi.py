@@ -55,3 +55,31 @@ def test_struct_layouts_match_header_order():
             decl = re.sub(r"^(const\s+)?\w+\s*", "", decl)
             fields += [f.strip().lstrip("*").strip() for f in decl.split(",")]
         assert fields == [f[0] for f in pyt._fields_], (cname, fields)
+
+
+def test_argument_checks_fail_before_any_device_call():
+    """Argument validation of the class-run entry points returns SCMP_E_ARG with a message,
+    before touching the device (runs without a GPU)."""
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(16)          # never dereferenced: the checks reject first
+    rc = lib.scmp_permute_code_columns(None, 4, 16, dummy, 16, dummy, 16, None)
+    assert rc == -1 and b"null" in lib.scmp_last_error()
+    rc = lib.scmp_permute_code_columns(dummy, 4, 16, dummy, 20, dummy, 24, None)
+    assert rc == -1 and b"multiple of 16" in lib.scmp_last_error()
+    g = _lib.GemmArgs()
+    g.ca = g.cb = g.lut = g.y = dummy.value
+    g.N, g.M, g.D, g.batch = 8, 8, 64, 1
+    g.lda = g.ldb = 64
+    g.JP, g.ldy = 64, 8
+    g.epi.kind = _lib.EPI_ROWCOL
+    g.impl = _lib.GEMM_MFMA_FP4
+    g.nclass = 2
+    g.group_class = dummy.value
+    g.chunk = 16                          # chunked accumulation and class runs do not mix
+    assert lib.scmp_sc_gemm(g, None) == -1 and b"group_class" in lib.scmp_last_error()
+    g.chunk = 0
+    g.d_class = dummy.value               # nor per-d classes and class runs
+    assert lib.scmp_sc_gemm(g, None) == -1 and b"group_class" in lib.scmp_last_error()
+    g.d_class = None
+    g.impl = _lib.GEMM_MFMA               # class runs are an FP4-kernel layout
+    assert lib.scmp_sc_gemm(g, None) == -1 and b"group_class" in lib.scmp_last_error()
