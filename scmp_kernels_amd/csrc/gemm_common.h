@@ -41,6 +41,7 @@ struct GemmP {
     int *cnt;
     const int64_t *row_map;   // output row of A row n (NULL: n)
     const int32_t *group_class;   // FP4: class of each 8-d group (NULL: none)
+    int row0;                 // chunked FP4 launch: first A row it computes
 };
 
 // Output row of A row n: the caller's row map scatters a row subset in place.

@@ -97,7 +97,10 @@ static int fp4_launch_jpf(const GemmP &P, int64_t batch, int JPF, bool chunked,
 int gemm_fp4_run(GemmP &P, const scmp_gemm_args &a, bool chunked, hipStream_t stream) {
     // 16-interval tables: four inner dimensions per MFMA k-step (JPF = 16), except in the
     // chunk_d kernel, whose chunk boundaries need only be even (JPF = 32)
-    if (chunked) return fp4_launch_jpf(P, a.batch, a.JP < 32 ? 32 : a.JP, true, stream);
+    if (chunked) {
+        P.nwg = device_cu_count();               // sizes the rounds of whole tiles
+        return fp4_launch_jpf(P, a.batch, a.JP < 32 ? 32 : a.JP, true, stream);
+    }
     const int JPF = a.JP;
     Fp4Plan plan = fp4_plan(a.N, a.M, a.D, a.batch, device_cu_count(), fp4_narrow_ok(a));
     P.tile_cols = plan.TC;

@@ -688,6 +688,7 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
     const int D = P.D;
     const int ngroups = (D + 7) / 8;
     const int nchunks = (D + P.chunk - 1) / P.chunk;
+    const int tr0 = P.row0 + ta * TR, tc0 = tb * TC;     // the tile's first row / column
     // SLDS: every chunk's scales of the tile's rows and columns sit in LDS
     // ([chunk][TR] then [chunk][TC], zero past N / M), so the chunk epilogue in the main
     // loop issues no global load (whose wait would also wait for the code loads in flight)
@@ -695,7 +696,6 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
     float *s_sb = s_sa + nchunks * TR;
     fp4_load_tables<JPF, LUTSRC, NT>(P, sA, sB);
     if (SLDS) {
-        const int tr0 = ta * TR, tc0 = tb * TC;
         for (int e = tid; e < nchunks * TR; e += NT) {
             const int k = e / TR, r = e - k * TR;
             s_sa[e] = tr0 + r < P.N ? P.epi.sa[(int64_t)k * P.epi.sa_chunk_stride + tr0 + r] : 0.f;
@@ -710,8 +710,8 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
     const int lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, li = lane & 31;
     const int wa = wave % WA, wb = wave / WA;
-    const int a0 = (ta * WA + wa) * (BA * 32);
-    const int b0 = (tb * WB + wb) * (BB * 32);
+    const int a0 = tr0 + wa * (BA * 32);
+    const int b0 = tc0 + wb * (BB * 32);
 
     const uint8_t *abase = P.ca + batch * P.bsa + (int64_t)a0 * P.lda;
     const uint8_t *bbase = P.cb + batch * P.bsb + (int64_t)b0 * P.ldb;
@@ -738,8 +738,8 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
         const float cc = P.epi.c;
         const float *sa = P.epi.sa + (int64_t)kchunk * P.epi.sa_chunk_stride;
         const float *sb = P.epi.sb + (int64_t)kchunk * P.epi.sb_chunk_stride;
-        const int lsa0 = (kchunk - ta) * TR;                 // s_sa[lsa0 + n]: row n
-        const int lsb0 = (kchunk - tb) * TC;                 // s_sb[lsb0 + m]: column m
+        const int lsa0 = kchunk * TR - tr0;                  // s_sa[lsa0 + n]: row n
+        const int lsb0 = kchunk * TC - tc0;                  // s_sb[lsb0 + m]: column m
 #pragma unroll
         for (int c = 0; c < BB; ++c) {
             const int m = b0 + 32 * c + li;
@@ -836,12 +836,13 @@ static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
     return SCMP_OK;
 }
 
-// Chunked: 128 x 128 tiles, each wave 64 x 64 (2 x 2 blocks, fp32 chunk sums in registers).
-template <int JPF, int LUTSRC>
-static int launch_fp4_chunked(const GemmP &P0, int64_t batch, hipStream_t stream) {
-    constexpr int BA = 2, BB = 2, WA = 2, WB = 2;
+// Chunked launch of rows [P.row0, P.N) in TR x 128 tiles, BA x 2 blocks of 32 x 32 per wave
+// (fp32 chunk sums in registers), one workgroup per tile.
+template <int JPF, int LUTSRC, int BA>
+static int launch_fp4_chunked_rows(const GemmP &P0, int64_t batch, hipStream_t stream) {
+    constexpr int BB = 2, WA = 2, WB = 2;
     GemmP P = P0;
-    P.tilesA = (int)cdiv(P.N, WA * BA * 32);
+    P.tilesA = (int)cdiv(P.N - P.row0, WA * BA * 32);
     const int64_t tilesB = cdiv(P.M, WB * BB * 32);
     const size_t tabs = (fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15;
     const size_t scales = (size_t)cdiv(P.D, P.chunk) * (WA * BA * 32 + WB * BB * 32) * sizeof(float);
@@ -855,6 +856,33 @@ static int launch_fp4_chunked(const GemmP &P0, int64_t batch, hipStream_t stream
            stream>>>(P);
     SCMP_LAUNCH_CHECK("scmp_sc_gemm(mfma fp4, chunked)");
     return SCMP_OK;
+}
+
+// Chunked: 128 x 128 tiles (each wave 64 x 64), one workgroup per tile and compute unit. The
+// inner dimension cannot be split (the fp32 chunk sums have a fixed order), so when the tiles
+// fill the compute units k + f times (0 < f < 1), the rows of the first k full rounds run as
+// 128 x 128 tiles and the rest as 64 x 128 tiles (each wave 32 x 64: half the MFMAs, three
+// quarters of the LDS reads), if that shortens the last round.
+template <int JPF, int LUTSRC>
+static int launch_fp4_chunked(const GemmP &P, int64_t batch, hipStream_t stream) {
+    const int64_t tilesB = cdiv(P.M, 128), total = cdiv(P.N, 128) * tilesB * batch;
+    const int64_t ncu = P.nwg;                            // compute units
+    const int64_t full = total / ncu;                     // complete rounds
+    if (full >= 1 && total % ncu != 0) {
+        const int64_t rows_main = full * ncu / (tilesB * batch) * 128;
+        const int64_t tail = cdiv(P.N - rows_main, 64) * tilesB * batch;
+        // time in 128 x 128 tile rounds: now full + 1; split: full + 0.75 per tail round
+        if (rows_main > 0 && rows_main < P.N && 4 * full + 3 * cdiv(tail, ncu) < 4 * (full + 1)) {
+            GemmP Pm = P;
+            Pm.N = (int)rows_main;                         // rows [0, rows_main)
+            int rc = launch_fp4_chunked_rows<JPF, LUTSRC, 2>(Pm, batch, stream);
+            if (rc != SCMP_OK) return rc;
+            GemmP Pt = P;
+            Pt.row0 = (int)rows_main;                      // rows [rows_main, N)
+            return launch_fp4_chunked_rows<JPF, LUTSRC, 1>(Pt, batch, stream);
+        }
+    }
+    return launch_fp4_chunked_rows<JPF, LUTSRC, 2>(P, batch, stream);
 }
 
 // Stream tables: one shared table in LDS; every class table in LDS when they fit

@@ -608,3 +608,18 @@ def test_permute_code_columns(rows, ld_in, ncols, ld_out):
     ref = np.zeros((rows, ld_out), np.uint8)
     ref[:, :ncols] = np.where(src >= 0, x[:, np.clip(src, 0, None)], 0)
     np.testing.assert_array_equal(out.cpu().numpy(), ref)
+
+
+def test_chunk_d_full_rounds_and_tail():
+    """chunk_d where 128 x 128 tiles fill the compute units 1.1 times (284 tiles on 256 CUs):
+    rows of the full round (128 x 128 tiles) and of the tail (64 x 128 tiles, rows 8192 on)
+    against the oracle, including the rows at the boundary and the last rows."""
+    from scmp_kernels_amd import sc_matmul
+    N, M, D = 9000, 500, 200
+    rng = np.random.default_rng(9000)
+    a = rng.standard_normal((N, D)).astype(np.float32)
+    b = (rng.standard_normal((M, D)) * 0.05).astype(np.float32)
+    y = sc_matmul(T(a), T(b), "per_row", mode="bipolar", chunk_d=48)
+    rows = np.r_[0:40, 8150:8260, 8960:9000]
+    ref = O.sc_matmul(a[rows], b, "per_row", mode="bipolar", chunk_d=48)
+    bits_equal(y[torch.from_numpy(rows).to(y.device)], ref)
