@@ -38,12 +38,15 @@ struct Fp4Plan {
 static Fp4Plan fp4_plan(int64_t N, int64_t M, int64_t D, int64_t batch, int ncu,
                         bool narrow_ok) {
     Fp4Plan p;
-    // tile counts of the two shapes (equal tile areas)
+    // tile counts of the two shapes (equal tile areas); wide tiles read B rows up to M
+    // rounded up to 512, within the buffer only when that equals M rounded up to 256 (the
+    // code buffers' row padding)
     const int64_t sq = cdiv(N, 256) * cdiv(M, 256), wide = cdiv(N, 128) * cdiv(M, 512);
+    const bool wide_fits = cdiv(M, 512) * 512 == cdiv(M, 256) * 256;
     if (narrow_ok && M <= 64) {
         p.TR = 256;
         p.TC = 64;
-    } else if (wide * 100 <= sq * 97) {
+    } else if (wide_fits && wide * 100 <= sq * 97) {
         p.TR = 128;
         p.TC = 512;
     } else {

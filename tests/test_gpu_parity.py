@@ -396,6 +396,18 @@ def _random_gemm_shapes(n):
     return out
 
 
+def test_gemm_wide_tile_padding_rule():
+    """Few rows and M = 2300 (M rounded up to 512 passes the 256-row padding of the code
+    buffers): 128 x 512 tiles would read B rows past the buffer, so the plan keeps 256 x 256
+    tiles; and M = 2560, where 128 x 512 tiles are taken."""
+    for N, M, D in ((100, 2300, 96), (100, 2560, 64)):
+        rng = np.random.default_rng(N + M)
+        a = rng.standard_normal((N, D)).astype(np.float32)
+        b = rng.standard_normal((M, D)).astype(np.float32)
+        got = _int_accum_gpu(a, b, L=64, R=64, bipolar=True, impl=2)
+        np.testing.assert_array_equal(got, _int_accum_ref(a, b, L=64, R=64, bipolar=True))
+
+
 @pytest.mark.parametrize("case", _random_gemm_shapes(12))
 def test_gemm_random_shapes_fp4(case):
     """Seeded random shapes through the default (FP4) kernel: whole and split tiles,
