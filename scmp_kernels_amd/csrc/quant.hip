@@ -59,6 +59,11 @@ __device__ __forceinline__ float wave_min(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
     return v;
 }
+// Sum over the wave; exact for the integer-valued code sums it is used on (below 2^24).
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
 
 // stats[unit*2 + 0] = key(max) or bits(max|x|); stats[unit*2 + 1] = key(-min)
 __global__ void reduce_kernel(scmp_quant_args a, int64_t group, int64_t segw, int64_t nseg,
@@ -473,6 +478,18 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
     const float rf = (float)a.rng_levels;
     const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
     const bool api_out = a.beta16 || a.beta32 || a.sign || a.xint;
+    // Row sums: with rows of a multiple of 64 chunks (and NT a multiple of 64) the chunks of
+    // one wave lie in one row and the wave is active as a whole, so it adds its sum with one
+    // LDS atomic instead of 64 on the same address. Integer-valued: exact in any order.
+    const bool wave_rows = cpr % 64 == 0;
+    auto add_rowsum = [&](int rr, float qs) __attribute__((always_inline)) {
+        if (wave_rows) {
+            const float w = wave_sum(qs);
+            if (lane == 0) atomicAdd(&rsums[rr], w);
+        } else {
+            atomicAdd(&rsums[rr], qs);
+        }
+    };
     // General element path: any chunk, any requested outputs.
     auto emit = [&](const float (&v)[4], int rr, int c) __attribute__((always_inline)) {
         const int64_t r = r0 + rr;
@@ -491,7 +508,7 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
             const int64_t b = r / cbr, i = r - b * cbr;
             *(uint32_t *)(a.code + (b * a.code_rows + i) * a.code_ld + c) = word;
         }
-        if (want_sum) atomicAdd(&rsums[rr], qs);
+        if (want_sum) add_rowsum(rr, qs);
     };
     // Hot path: full chunks, GEMM codes only (jtab in LDS). The four quotients take the
     // multiply-by-reciprocal route together; one branch per chunk redoes all four with
@@ -541,7 +558,7 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
             qs += q;
         }
         *(uint32_t *)(crow + c) = word;
-        if (want_sum) atomicAdd(&rsums[rr], qs);
+        if (want_sum) add_rowsum(rr, qs);
     };
     const bool fast = !api_out && a.code && !(thermo && !lds_jtab);
     if (fast) {
