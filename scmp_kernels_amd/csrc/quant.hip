@@ -510,7 +510,8 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         }
         if (want_sum) add_rowsum(rr, qs);
     };
-    // Hot path: full chunks, GEMM codes only (jtab in LDS). The four quotients take the
+    // Hot path: GEMM codes only (jtab in LDS, or per-column classes' rows of jtab read from
+    // global memory). The four quotients take the
     // multiply-by-reciprocal route together; one branch per chunk redoes all four with
     // the exact division when any of them is within reach of a half-integer (see
     // rne_quotient for the bound).
@@ -543,13 +544,26 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         const int nv = a.cols - c;
         uint32_t word = 0;
         float qs = 0.0f;
+        // per-column table classes: the chunk's four classes (one 16-byte load for a full
+        // chunk), each code from its class's row of jtab
+        int cls[4] = {0, 0, 0, 0};
+        if (thermo && !lds_jtab) {
+            if (nv >= 4) {
+                const int4 c4 = *(const int4 *)(a.col_class + c);
+                cls[0] = c4.x; cls[1] = c4.y; cls[2] = c4.z; cls[3] = c4.w;
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) cls[k] = k < nv ? a.col_class[c + k] : 0;
+            }
+        }
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const float q = k < nv ? fmin_first(fmax_first(t[k], qlo), qf) : 0.0f;
             const int qi = (int)q;
             uint32_t code;
             if (thermo) {
-                code = s_jtab[qi < 0 ? -qi : qi];
+                const int mi = qi < 0 ? -qi : qi;
+                code = lds_jtab ? s_jtab[mi] : a.jtab[(int64_t)cls[k] * 256 + mi];
                 if (!asym && qi < 0) code |= 0x80u;
             } else {
                 code = (uint32_t)(qi & 0xff);
@@ -560,7 +574,9 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         *(uint32_t *)(crow + c) = word;
         if (want_sum) add_rowsum(rr, qs);
     };
-    const bool fast = !api_out && a.code && !(thermo && !lds_jtab);
+    // per-column classes are read with 16-byte loads: col_class 16-byte aligned
+    const bool fast = !api_out && a.code &&
+                      (lds_jtab || !thermo || ((uintptr_t)a.col_class & 15) == 0);
     if (fast) {
         // code row of input row r0 + rr: batch bb, row bi of the batch; tracked as rr grows
         // (a step that leaves a batch skips that batch's padding rows)
