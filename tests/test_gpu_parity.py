@@ -567,6 +567,29 @@ def test_sc_matmul_class_runs_chosen(kw, shape, monkeypatch):
     bits_equal(sc_matmul(T(a), T(b), "per_row", **kw), O.sc_matmul(a, b, "per_row", **kw))
 
 
+@pytest.mark.parametrize("gran,kw,shape", [
+    ("per_tensor", dict(mode="unipolar", stoc_len=64, rng_levels=64), (70, 90, 1024)),
+    ("per_tensor", dict(mode="bipolar", stoc_len=64, rng_levels=64), (65, 40, 512)),
+    ("per_row", dict(mode="unipolar", stoc_len=32, rng_levels=32, smooth=True), (50, 70, 520)),
+])
+def test_sc_matmul_class_runs_other_epilogues(gran, kw, shape, monkeypatch):
+    """The run layout (forced) under the scalar and zero-point epilogues, whose correction
+    terms use the true inner dimension, not the padded one the GEMM runs over."""
+    from scmp_kernels_amd import sc_matmul
+    monkeypatch.setenv("SCMP_FP4_RUNS", "1")
+    N, M, D = shape
+    rng = np.random.default_rng(N + M + D + 7)
+    a = rng.standard_normal((N, D)).astype(np.float32)
+    b = (rng.standard_normal((M, D)) * 0.05).astype(np.float32)
+    kw = dict(kw)
+    if kw.pop("smooth", False):
+        kw["smooth_scales"] = rng.uniform(0.5, 2.0, D).astype(np.float32)
+        y = sc_matmul(T(a), T(b), gran, **dict(kw, smooth_scales=T(kw["smooth_scales"])))
+    else:
+        y = sc_matmul(T(a), T(b), gran, **kw)
+    bits_equal(y, O.sc_matmul(a, b, gran, **kw))
+
+
 def test_class_runs_equal_global_tables_full_size(monkeypatch):
     """cfg5's L=64 level shape (1365 x 4096 x 4096, unipolar, groups of 4): the run layout
     and the per-d global-table path give the same bits."""
