@@ -36,7 +36,7 @@ struct GemmP {
     // (ntiles ints, zero on entry)
     int tile_cols;
     int64_t ntiles;
-    int nwg;
+    int nwg;                  // persistent workgroups (chunked launch: compute units)
     float *part;
     int *cnt;
     const int64_t *row_map;   // output row of A row n (NULL: n)
