@@ -504,6 +504,16 @@ def test_per_head_vs_oracle(shape):
     bits_equal(y, O.sc_matmul(q, k, "per_head"))
 
 
+def test_per_row_3d_wide_tiles_vs_oracle():
+    """Batched operands whose per-batch output (300 x 500) takes 128 x 512 tiles."""
+    from scmp_kernels_amd import sc_matmul
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal((3, 300, 96)).astype(np.float32)
+    b = rng.standard_normal((3, 500, 96)).astype(np.float32)
+    for kw in (dict(mode="bipolar"), dict(mode="unipolar", stoc_len=64, rng_levels=64)):
+        bits_equal(sc_matmul(T(a), T(b), "per_row", **kw), O.sc_matmul(a, b, "per_row", **kw))
+
+
 def test_per_row_3d_vs_oracle():
     from scmp_kernels_amd import sc_matmul
     rng = np.random.default_rng(11)
