@@ -244,8 +244,8 @@ int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream);
 int64_t scmp_sc_gemm_workspace_bytes(const scmp_gemm_args *args);
 
 /* FP4 (e2m1) form of a stream table for SCMP_GEMM_MFMA_FP4: JPF = max(JP, 32) nibbles per
- * row (JPF / 2 bytes), dword u nibble b holds interval j' = (JP/8)*b + u (JP = 16: dwords 0
- * and 1, dwords 2 and 3 zero). Counts that e2m1 cannot represent exactly (anything but 0, 1,
+ * row (JPF / 2 bytes), dword u nibble b holds interval j' = 8u + b (JP = 16: dwords 0 and 1,
+ * dwords 2 and 3 zero). Counts that e2m1 cannot represent exactly (anything but 0, 1,
  * 2, 3, 4, 6) set *bad to 1; the table is then unusable and the int8 kernel must be used. */
 int scmp_build_fp4_lut(const int8_t *lut, int nclass, int JP, uint8_t *lut4, int32_t *bad,
                        hipStream_t stream);

@@ -139,7 +139,7 @@ __global__ void fp4_lut_kernel(const int8_t *lut, int nclass, int JP, int JPF, u
     uint32_t out = 0;
     for (int k = 0; k < 2; ++k) {
         const int b = 2 * pair + k;
-        const int jp = U4 * b + u;
+        const int jp = 8 * u + b;
         int v = 0;
         if (u < U4 && jp < JP) v = lut[cr * JP + 4 * (jp % U8) + jp / U8];
         const int mag = v < 0 ? -v : v;
