@@ -182,6 +182,8 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     constexpr int ROWB = G::ROWB, KSU = G::KSU, SPD = G::SPD, UPG = G::UPG, LS = G::LS,
                   TAB = G::TAB;
     constexpr int NR = BA + BB;                  // code rows per lane: A rows, then B rows
+    // VALU slots per MFMA in the pinned interleave (two for JPF >= 128: 0.4% at cfg2)
+    constexpr int NVS = JPF >= 128 ? 2 : 1;
     constexpr bool PERD = LUTSRC == LUT_LDS_CLASSES || LUTSRC == LUT_GLOBAL;   // per-d classes
     const uint8_t *glut = (const uint8_t *)P.lut;
     const int D = P.D;
@@ -358,7 +360,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             stage(F1, ca, cls, qb, m, uu + 1, dg);
             mma(F0);
             if (SCHED) {
-                interleave_unit<BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1), 1>();
+                interleave_unit<BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1), NVS>();
                 __builtin_amdgcn_sched_barrier(0);
             }
             done(uu, dg);
@@ -374,7 +376,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             }
             mma(F1);
             if (SCHED) {
-                interleave_unit<BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1), 1>();
+                interleave_unit<BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1), NVS>();
                 __builtin_amdgcn_sched_barrier(0);
             }
             done(uu + 1, dg);
