@@ -165,8 +165,8 @@ def _fp4_class_runs(tabs: "_tables.StreamTables", D: int):
     if env != "1" and tab * (1 + tabs.nclass) + _FP4_STAGE_BYTES <= _FP4_MAX_LDS:
         return None                              # every class table fits in LDS
     runs = tabs.class_runs()
-    if env != "1" and runs[2] > D + D // 8:
-        return None
+    if runs[2] > 65536 or (env != "1" and runs[2] > D + D // 8):
+        return None                              # the FP4 kernel's exact range: D <= 65536
     return runs
 
 

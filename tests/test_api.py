@@ -231,3 +231,7 @@ def test_class_runs_selection(monkeypatch):
     assert K._fp4_class_runs(_fake_tables(np.arange(256) % 64), 256)[2] == 512
     monkeypatch.setenv("SCMP_FP4_RUNS", "0")
     assert K._fp4_class_runs(t, 4096) is None
+    # not even when forced do runs pad D past the FP4 kernel's 65536 (here 5000 classes of
+    # 13-14 d each: 65500 -> 80000)
+    monkeypatch.setenv("SCMP_FP4_RUNS", "1")
+    assert K._fp4_class_runs(_fake_tables(np.arange(65500) % 5000), 65500) is None
