@@ -243,6 +243,20 @@ int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream);
  * scmp_kernels/sc/kernels.py:838-866). */
 int64_t scmp_sc_gemm_workspace_bytes(const scmp_gemm_args *args);
 
+/* scmp_sc_gemm without any allocation: the same kernels and results, with the FP4 kernel's
+ * split-tile workspace taken from a static device array of the library
+ * (SCMP_SC_GEMM_NOALLOC_SCRATCH_BYTES per device, held from the library's first use of
+ * the device until the process ends) instead of from the caller. args->workspace must be
+ * NULL and args->workspace_bytes 0. A problem whose scmp_sc_gemm_workspace_bytes exceeds
+ * the scratch returns SCMP_E_ARG before any device work. The scratch keeps the last
+ * call's contents; the library clears what must start at zero (the tile counters, by a
+ * kernel on the stream). Every call on one device shares that device's scratch, so calls
+ * that overlap on one device (different streams or host threads) race.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+#define SCMP_SC_GEMM_NOALLOC_SCRATCH_BYTES ((int64_t)129 << 20)
+int scmp_sc_gemm_noalloc(const scmp_gemm_args *args, hipStream_t stream);
+
 /* FP4 (e2m1) form of a stream table for SCMP_GEMM_MFMA_FP4: JPF = max(JP, 32) nibbles per
  * row (JPF / 2 bytes), dword u nibble b holds interval j' = 8u + b (JP = 16: dwords 0 and 1,
  * dwords 2 and 3 zero). Counts that e2m1 cannot represent exactly (anything but 0, 1,

@@ -19,6 +19,7 @@ c_float = ctypes.c_float
 c_vp = ctypes.c_void_p
 
 SCMP_OK = 0
+SCMP_E_ARG = -1
 
 # quantizer variants / modes (scmp_hip.h)
 (Q_GROUP_SYM, Q_ROW_SYM, Q_TENSOR_SYM, Q_HEAD_SYM, Q_GROUP_ASYM, Q_TENSOR_ASYM, Q_HOST_SYM,
@@ -73,7 +74,10 @@ EXPORTS = [
     "scmp_rng_expand", "scmp_rng_prepare", "scmp_lfsr_search", "scmp_build_stream_tables",
     "scmp_quant_workspace_bytes", "scmp_quantize", "scmp_sc_gemm", "scmp_build_bitlut",
     "scmp_build_fp4_lut", "scmp_sc_gemm_workspace_bytes", "scmp_permute_code_columns",
+    "scmp_sc_gemm_noalloc",
 ]
+
+SC_GEMM_NOALLOC_SCRATCH_BYTES = 129 << 20   # SCMP_SC_GEMM_NOALLOC_SCRATCH_BYTES
 
 _lib = None
 _lock = threading.Lock()
@@ -106,6 +110,7 @@ def load(path: str = LIB_PATH):
         lib.scmp_quant_workspace_bytes.restype = c_i64
         lib.scmp_quantize.argtypes = [ctypes.POINTER(QuantArgs), c_vp]
         lib.scmp_sc_gemm.argtypes = [ctypes.POINTER(GemmArgs), c_vp]
+        lib.scmp_sc_gemm_noalloc.argtypes = [ctypes.POINTER(GemmArgs), c_vp]
         lib.scmp_sc_gemm_workspace_bytes.argtypes = [ctypes.POINTER(GemmArgs)]
         lib.scmp_sc_gemm_workspace_bytes.restype = c_i64
         lib.scmp_build_bitlut.argtypes = [c_vp, c_int, c_int, c_vp, c_vp]

@@ -186,6 +186,26 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
             row_map=None):
     """scmp_sc_gemm on the current stream. ca / cb are code buffers (batch, rows_pad, ld)
     or (rows_pad, ld)."""
+    g, keep = sc_gemm_args(ca, cb, N=N, M=M, D=D, batch=batch, tabs=tabs, epi=epi, y=y,
+                           iout=iout, ldy=ldy, bsy=bsy, chunk=chunk, d_class=d_class,
+                           impl=impl, tile=tile, row_map=row_map)
+    lib = _lib.load()
+    ws = None
+    nbytes = int(lib.scmp_sc_gemm_workspace_bytes(g))
+    if nbytes > 0:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=ca.device)
+        g.workspace, g.workspace_bytes = ws.data_ptr(), nbytes
+    _lib.check(lib.scmp_sc_gemm(g, _lib.stream_of(ca.device)), "scmp_sc_gemm")
+    return ws, keep  # keep the buffers alive until the stream has consumed them
+
+
+def sc_gemm_args(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables",
+                 epi: "_lib.Epilogue", y=None, iout=None, ldy=None, bsy=0, chunk=0,
+                 d_class=None, impl=None, tile=None, row_map=None):
+    """The scmp_gemm_args of one SC GEMM (workspace not yet attached) and the device
+    buffers it points to, which must stay alive until the stream has consumed them.
+    Chooses the kernel and, for the FP4 kernel with per-d classes, the class-run layout
+    (launching the code permutation on the current stream)."""
     dev = ca.device
     stream = _lib.stream_of(dev)
     if impl is None:
@@ -229,14 +249,7 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
     g.tile = int(os.environ.get("SCMP_GEMM_TILE", "0")) if tile is None else tile
     if g.impl == _lib.GEMM_VALU:
         g.bitlut = tabs.bitlut(stream).data_ptr()
-    lib = _lib.load()
-    ws = None
-    nbytes = int(lib.scmp_sc_gemm_workspace_bytes(g))
-    if nbytes > 0:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        g.workspace, g.workspace_bytes = ws.data_ptr(), nbytes
-    _lib.check(lib.scmp_sc_gemm(g, stream), "scmp_sc_gemm")
-    return ws, ca, cb  # keep the buffers alive until the stream has consumed them
+    return g, (ca, cb)
 
 
 def _codes(rows: int, D: int, device, batch: int = 0) -> torch.Tensor:
