@@ -195,10 +195,13 @@ def make_sobol_simple_config(q_e: int, k_e: int, sc_prec: int = 8) -> dict:
 OWEN_SEED = 0x5A5A5A5A  # scmp_kernels/sc/kernels.py:635
 
 
-def owen_masks(D: int, base: int, mode: str = "bitrev") -> Optional[np.ndarray]:
+def owen_masks(D: int, base: int, mode: str = "bitrev", device="cpu") -> Optional[np.ndarray]:
     """scmp_kernels/sc/kernels.py:646-670. Returns per-d XOR masks or None (off).
-    'random' draws from torch's CPU generator (the reference uses the operand device's
-    generator; the CPU stream is what this build reproduces, documented deviation)."""
+    'random' is torch.randint(0, base, (D, 1)) from torch.Generator(device) seeded with
+    0x5A5A5A5A, the generator of the device the sequences live on (kernels.py:664-668):
+    "cpu" is the reference's draw for CPU tensors (pinned by a reference-run golden vector);
+    a GPU device gives torch's device generator, which the product uses for device tensors
+    (the values of that generator are torch's, not restated here)."""
     mode = mode.lower()
     if mode == "off":
         return None
@@ -208,17 +211,19 @@ def owen_masks(D: int, base: int, mode: str = "bitrev") -> Optional[np.ndarray]:
     if mode == "bitrev":
         nbits = int(round(math.log2(base)))
         return np.array([lib().orc_bitrev(int(i), nbits) for i in idx], dtype=np.int32)
-    import torch  # 'random': torch.Generator(cpu).manual_seed(seed); randint(0, base, (D, 1))
-    g = torch.Generator().manual_seed(OWEN_SEED)
-    return torch.randint(0, base, (D, 1), generator=g).reshape(D).numpy().astype(np.int32)
+    import torch
+    g = torch.Generator(device=device).manual_seed(OWEN_SEED)
+    m = torch.randint(0, base, (D, 1), generator=g, device=device)
+    return m.reshape(D).cpu().numpy().astype(np.int32)
 
 
 def prepare_prefix(r: np.ndarray, sc_prec: int, L: int, R: int, owen_mode: str = "bitrev",
-                   scramble_rescale: bool = True) -> np.ndarray:
+                   scramble_rescale: bool = True, owen_device="cpu") -> np.ndarray:
     """_prepare_rng_prefix, scmp_kernels/sc/kernels.py:673-704. r: (D, 2^p) int32."""
     r = np.ascontiguousarray(r, dtype=np.int32)
     D, full = r.shape
-    masks = owen_masks(D, 2 ** sc_prec, owen_mode)
+    needs_mask = (L < full) if R == 2 ** sc_prec else scramble_rescale
+    masks = owen_masks(D, 2 ** sc_prec, owen_mode, owen_device) if needs_mask else None
     out = np.zeros((D, L), dtype=np.int32)
     lib().orc_prepare_prefix(_p(r), ctypes.c_int(D), ctypes.c_int(full), ctypes.c_int(sc_prec),
                              ctypes.c_int(L), ctypes.c_int(R),
@@ -269,11 +274,14 @@ class Tables:
     (the reference stores D copies; values are the same)."""
 
     def __init__(self, config: dict, sc_prec: int, L: int, R: int,
-                 owen_mode: str = "bitrev", scramble_rescale: bool = True):
+                 owen_mode: str = "bitrev", scramble_rescale: bool = True,
+                 owen_device="cpu"):
         ra_full = sng_sequences(config, "q", sc_prec)
         rb_full = sng_sequences(config, "k", sc_prec)
-        self.ra = prepare_prefix(ra_full, sc_prec, L, R, owen_mode, scramble_rescale)
-        self.rb = prepare_prefix(rb_full, sc_prec, L, R, owen_mode, scramble_rescale)
+        self.ra = prepare_prefix(ra_full, sc_prec, L, R, owen_mode, scramble_rescale,
+                                 owen_device)
+        self.rb = prepare_prefix(rb_full, sc_prec, L, R, owen_mode, scramble_rescale,
+                                 owen_device)
         self.L, self.R = L, R
         self.V = next_pow2(R + 1)  # scmp_kernels/sc/kernels.py:737-739
         self.tab_of, uniq = dedupe_rows(self.ra, self.rb)
@@ -495,14 +503,17 @@ class Ctx:
     """Options that the reference reads from the environment per call
     (scmp_kernels/sc/kernels.py:648-701)."""
 
-    def __init__(self, owen_mode="bitrev", scramble_rescale=True, nthreads=1):
+    def __init__(self, owen_mode="bitrev", scramble_rescale=True, nthreads=1,
+                 owen_device="cpu"):
         self.owen_mode = owen_mode
         self.scramble_rescale = scramble_rescale
         self.nthreads = nthreads
+        self.owen_device = owen_device   # device whose generator draws 'random' masks
 
 
 def _tables(config, sc_prec, L, R, ctx):
-    return Tables(config, sc_prec, L, R, ctx.owen_mode, ctx.scramble_rescale)
+    return Tables(config, sc_prec, L, R, ctx.owen_mode, ctx.scramble_rescale,
+                  ctx.owen_device)
 
 
 def sc_matmul(a, b, granularity="per_row", *, mode="bipolar", sc_prec=8, stoc_len=None,

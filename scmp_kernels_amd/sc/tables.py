@@ -58,10 +58,10 @@ def scramble_rescale_from_env() -> bool:
 _OWEN_SEED = 0x5A5A5A5A  # scmp_kernels/sc/kernels.py:635
 
 
-def owen_masks(D: int, base: int, mode: str) -> Optional[np.ndarray]:
-    """Per-dimension XOR masks, scmp_kernels/sc/kernels.py:655-670. 'random' draws from
-    torch's CPU generator with the reference's seed (the reference draws on the operand's
-    device; the CPU stream is the one reproduced here)."""
+def owen_masks(D: int, base: int, mode: str, device="cpu") -> Optional[np.ndarray]:
+    """Per-dimension XOR masks, scmp_kernels/sc/kernels.py:655-670. 'random' draws
+    randint(0, base, (D, 1)) from a generator of the device the sequences live on, seeded
+    with the reference's seed (kernels.py:664-668: torch.Generator(device=prefix.device))."""
     if mode == "off":
         return None
     idx = np.arange(D, dtype=np.int64) % base
@@ -73,8 +73,9 @@ def owen_masks(D: int, base: int, mode: str) -> Optional[np.ndarray]:
         for i in range(nbits):
             out |= ((idx >> i) & 1) << (nbits - 1 - i)
         return out.astype(np.int32)
-    g = torch.Generator().manual_seed(_OWEN_SEED)
-    return torch.randint(0, base, (D, 1), generator=g).reshape(D).numpy().astype(np.int32)
+    g = torch.Generator(device=device).manual_seed(_OWEN_SEED)
+    m = torch.randint(0, base, (D, 1), generator=g, device=device)
+    return m.reshape(D).cpu().numpy().astype(np.int32)
 
 
 def beta_of_q(q: np.ndarray, Q: int, R: int) -> np.ndarray:
@@ -275,7 +276,7 @@ def get_tables(config: Optional[dict], default_desc: tuple, make_config, sc_prec
     rb_full = side_sequences(config, "k", sc_prec, D, device)
     base = 2 ** sc_prec
     needs_mask = (L < base) if R == base else True
-    masks = owen_masks(D, base, owen_mode_from_env()) if needs_mask else None
+    masks = owen_masks(D, base, owen_mode_from_env(), device) if needs_mask else None
     srs = scramble_rescale_from_env()
     ra = prepare(ra_full, sc_prec, L, R, masks, srs)
     rb = prepare(rb_full, sc_prec, L, R, masks, srs)

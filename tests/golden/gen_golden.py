@@ -62,11 +62,62 @@ def _normal(rng, shape, scale=1.0):
     return (rng.standard_normal(shape) * scale).astype(np.float32)
 
 
+def _time_cfg1(out_dir, sc_matmul, clear_rng_cache, a, b, torch):
+    """Time the reference's own cfg1 call (per_tensor bipolar, (32,256) x (64,256), L=256)
+    under the interpreter: one cold call (sequences and tables built) and five warm calls
+    (cached), wall clock. Written to ref_cpu_timing.json with the host description."""
+    import platform
+    import time
+    import triton as _triton
+    kw = {"granularity": "per_tensor", "sc_prec": 8, "stoc_len": 256}
+    clear_rng_cache()
+    t0 = time.perf_counter()
+    sc_matmul(a, b, **kw)
+    cold = time.perf_counter() - t0
+    warm = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        sc_matmul(a, b, **kw)
+        warm.append(time.perf_counter() - t0)
+    clear_rng_cache()
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    warm_s = sorted(warm)[len(warm) // 2]
+    rec = {
+        "what": "reference sc_matmul, BASELINE cfg1: per_tensor bipolar a(32,256) x b(64,256), "
+                "sc_prec=8, stoc_len=256, under TRITON_INTERPRET=1 on the CPU",
+        "sc_bitops_per_call": 32 * 64 * 256 * 256,
+        "cold_s": round(cold, 4), "warm_median_s": round(warm_s, 4),
+        "warm_sc_bitops_per_s": 32 * 64 * 256 * 256 / warm_s,
+        "warm_s": [round(w, 4) for w in warm],
+        "cores": 1,
+        "cores_note": "the Triton interpreter runs each program instance in one Python "
+                      "thread; torch.get_num_threads()=%d for the torch ops around it"
+                      % torch.get_num_threads(),
+        "host": {"cpu": cpu, "os_cpu_count": os.cpu_count(), "python": platform.python_version(),
+                 "torch": torch.__version__, "triton": _triton.__version__,
+                 "numpy": np.__version__},
+    }
+    with open(os.path.join(out_dir, "ref_cpu_timing.json"), "w") as f:
+        json.dump(rec, f, indent=1)
+    print(f"cfg1 reference timing: cold {cold:.3f} s, warm median {warm_s:.3f} s", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
     ap.add_argument("--out", default=os.path.dirname(os.path.abspath(__file__)))
+    ap.add_argument("--only", default="",
+                    help="comma-separated case names to (re)write; the others keep their "
+                         "files and cases.json entries")
+    ap.add_argument("--time-cfg1", action="store_true",
+                    help="also time the reference's cfg1 sc_matmul (ref_cpu_timing.json)")
     args = ap.parse_args()
+    only = set(filter(None, args.only.split(",")))
     torch = _install_shims(args.ref)
     from scmp_kernels import sc_matmul
     from scmp_kernels.sc import clear_rng_cache
@@ -75,11 +126,17 @@ def main():
     from scmp_kernels.sc.config_helpers import make_sobol_simple_config
 
     cases = {}
+    cases_path = os.path.join(args.out, "cases.json")
+    if only and os.path.exists(cases_path):
+        with open(cases_path) as f:
+            cases = json.load(f)
 
     def T(x):
         return torch.from_numpy(np.ascontiguousarray(x))
 
     def save(name, meta, **arrs):
+        if only and name not in only:
+            return
         path = os.path.join(args.out, f"{name}.npz")
         np.savez_compressed(path, **{k: np.asarray(v) for k, v in arrs.items()})
         cases[name] = meta
@@ -87,6 +144,8 @@ def main():
                                             for k, v in arrs.items()), flush=True)
 
     def run_matmul(name, a, b, kwargs, env=None, smooth=None):
+        if only and name not in only:
+            return
         env = env or {}
         old = {k: os.environ.get(k) for k in env}
         os.environ.update(env)
@@ -114,6 +173,9 @@ def main():
     b = _normal(rng, (64, 256))
     run_matmul("cfg1_per_tensor_bipolar", a, b,
                {"granularity": "per_tensor", "sc_prec": 8, "stoc_len": 256})
+
+    if args.time_cfg1:
+        _time_cfg1(args.out, sc_matmul, clear_rng_cache, T(a), T(b), torch)
 
     rng = np.random.default_rng(101)
     run_matmul("per_tensor_unipolar", _normal(rng, (8, 64)), _normal(rng, (16, 64), 0.5),
@@ -174,6 +236,51 @@ def main():
                {"granularity": "per_row", "sc_prec": 8})
     run_matmul("per_row_3d_unipolar", _normal(rng, (2, 4, 32)), _normal(rng, (2, 3, 32)),
                {"granularity": "per_row", "mode": "unipolar", "sc_prec": 8})
+
+    # --- RNG configurations other than the default Sobol (sc/sng.py:15-53, 187-230;
+    #     sc/rng.py:32-113; Owen 'random', sc/kernels.py:664-668) ---------------------------
+    import random as _random
+    pr = _random.Random(2024)
+
+    def perm8():
+        p = list(range(8))
+        pr.shuffle(p)
+        return p
+
+    D = 24
+    q_s = [perm8() if i % 3 else None for i in range(D)]
+    k_s = [perm8() if i % 2 else None for i in range(D)]
+    cfg_shared = {"rng_pool": [{"type": "lfsr", "seed": 45, "taps": [7, 5, 4, 3]}],
+                  "sng": {"q": [{"rng_id": 0, "scramble": s} for s in q_s],
+                          "k": [{"rng_id": 0, "scramble": s} for s in k_s]}}
+    cfg_multi = {"rng_pool": [{"type": "lfsr", "seed": 45, "taps": [7, 5, 4, 3]},
+                              {"type": "lfsr", "seed": 3, "taps": [7, 6, 5, 0]},
+                              {"type": "sobol", "seed_type": "k"}],
+                 "sng": {"q": [{"rng_id": i % 2, "scramble": q_s[i]} for i in range(D)],
+                         "k": [{"rng_id": 1 + i % 2, "scramble": k_s[i]} for i in range(D)]}}
+    cfg_true = {"rng_pool": [{"type": "true_random", "seed": 7},
+                             {"type": "true_random", "seed": 8}],
+                "sng": {"q": [{"rng_id": 0, "scramble": None} for _ in range(D)],
+                        "k": [{"rng_id": 1, "scramble": None} for _ in range(D)]}}
+    rng = np.random.default_rng(111)
+    a, b = _normal(rng, (6, D)), _normal(rng, (5, D))
+    run_matmul("per_row_bipolar_lfsr_shared_scrambled", a, b,
+               {"granularity": "per_row", "sc_prec": 8, "config": cfg_shared})
+    run_matmul("per_row_bipolar_multi_rng_scrambled", a, b,
+               {"granularity": "per_row", "sc_prec": 8, "config": cfg_multi})
+    run_matmul("per_row_unipolar_multi_rng_L64", a, b,
+               {"granularity": "per_row", "mode": "unipolar", "sc_prec": 8, "group_a": 2,
+                "group_b": 2, "stoc_len": 64, "rng_levels": 64, "config": cfg_multi})
+    run_matmul("per_row_bipolar_true_random", a, b,
+               {"granularity": "per_row", "sc_prec": 8, "config": cfg_true})
+    rng = np.random.default_rng(112)
+    a, b = _normal(rng, (7, 40)), _normal(rng, (6, 40))
+    run_matmul("per_row_bipolar_L64_owen_random", a, b,
+               {"granularity": "per_row", "sc_prec": 8, "stoc_len": 64, "rng_levels": 64},
+               env={"SC_OWEN_MODE": "random"})
+    run_matmul("per_row_bipolar_prefix64_owen_random", a, b,
+               {"granularity": "per_row", "sc_prec": 8, "stoc_len": 64},
+               env={"SC_OWEN_MODE": "random"})
 
     # --- integer accumulator straight from the tiled kernel (q_max_sq = stoc_len) --------
     rng = np.random.default_rng(109)
@@ -244,7 +351,7 @@ def main():
                                              "G": G, "q_max": 127},
              x=x3, scale=s_.numpy(), x_int=xi.numpy(), sign=sg.numpy())
 
-    with open(os.path.join(args.out, "cases.json"), "w") as f:
+    with open(cases_path, "w") as f:
         json.dump(cases, f, indent=1, sort_keys=True)
     print(f"{len(cases)} cases", flush=True)
 

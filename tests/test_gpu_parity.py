@@ -70,8 +70,8 @@ def test_prepare_prefix(L, R, mode, srs):
     ref_full = O.sng_sequences(cfg, "k", 8)
     got_full = TB.side_sequences(cfg, "k", 8, D, _dev())
     bits_equal(got_full, ref_full)
-    masks = TB.owen_masks(D, 256, mode)
-    ref_masks = O.owen_masks(D, 256, mode)
+    masks = TB.owen_masks(D, 256, mode, _dev())
+    ref_masks = O.owen_masks(D, 256, mode, _dev())
     if masks is None:
         assert ref_masks is None
     else:
@@ -458,7 +458,28 @@ def test_sc_matmul_golden(name, monkeypatch):
         kw["smooth_scales"] = T(z["smooth"])
     y = sc_matmul(T(z["a"]), T(z["b"]), **kw)
     clear_rng_cache()
+    if meta["env"].get("SC_OWEN_MODE") == "random":
+        # The reference draws 'random' Owen masks from the generator of the device its
+        # sequences live on (sc/kernels.py:664-668): the vector, written on the CPU, pins
+        # the oracle with the CPU generator; on the GPU both sides use the device's.
+        kw.pop("smooth_scales", None)
+        gran = kw.pop("granularity")
+        ref = O.sc_matmul(z["a"], z["b"], gran, smooth_scales=z.get("smooth"),
+                          ctx=O.Ctx(owen_mode="random", owen_device=_dev()), **kw)
+        bits_equal(y, ref)
+        return
     bits_equal(y, z["y"])
+
+
+def test_owen_random_masks_use_the_device_generator():
+    """The product's 'random' masks are torch.randint on the sequences' device with the
+    reference's seed (sc/kernels.py:664-668), and differ from the CPU generator's."""
+    from scmp_kernels_amd.sc import tables as TB
+    g = torch.Generator(device=_dev()).manual_seed(0x5A5A5A5A)
+    want = torch.randint(0, 256, (300, 1), generator=g, device=_dev()).reshape(-1)
+    got = TB.owen_masks(300, 256, "random", _dev())
+    np.testing.assert_array_equal(got, want.cpu().numpy())
+    assert not np.array_equal(got, TB.owen_masks(300, 256, "random", "cpu"))
 
 
 RANDOM_CASES = [

@@ -65,6 +65,89 @@ def test_lfsr_rejects_zero_seed():
         O.lfsr_sequence(8, 0, [0, 2, 3, 4], 8)
 
 
+# ------------------------------------------------------------------ SNG scrambles
+
+def _bits(v, n):
+    return [(int(v) >> i) & 1 for i in range(n)]
+
+
+def test_scramble_identity_and_reversal():
+    """The identity permutation leaves p-bit values unchanged; reverse_permutation(p) of
+    scmp_kernels/sc/sng.py:56-58, [p-1, ..., 0], is p-bit reversal."""
+    vals = np.arange(256, dtype=np.int32)
+    np.testing.assert_array_equal(O.scramble(vals, list(range(8))), vals)
+    rev = [int(f"{v:08b}"[::-1], 2) for v in range(256)]
+    assert O.scramble(vals, list(range(7, -1, -1))).tolist() == rev
+    rev5 = [int(f"{v:05b}"[::-1], 2) for v in range(32)]
+    assert O.scramble(np.arange(32, dtype=np.int32), [4, 3, 2, 1, 0]).tolist() == rev5
+
+
+def test_scramble_direction_known_answer():
+    """Output bit i takes source bit perm[i] (sng.py:21-28). perm = [1, 2, 0]: value 1
+    (bit 0 set) lands on output bit 2 (perm[2] = 0), so 1 -> 4; the opposite direction
+    (output bit perm[i] <- source bit i) would give 1 -> 2."""
+    got = O.scramble(np.array([1, 2, 4, 3, 6, 5, 7, 0], dtype=np.int32), [1, 2, 0])
+    assert got.tolist() == [4, 1, 2, 5, 3, 6, 7, 0]
+
+
+def test_scramble_inverse_round_trip_and_transposition():
+    rng = np.random.default_rng(17)
+    vals = rng.integers(0, 256, 500).astype(np.int32)
+    for _ in range(5):
+        perm = rng.permutation(8).tolist()
+        inv = np.argsort(perm).tolist()            # perm[inv[i]] == i
+        np.testing.assert_array_equal(O.scramble(O.scramble(vals, perm), inv), vals)
+        # popcount is invariant under any bit permutation
+        assert [bin(v).count("1") for v in O.scramble(vals, perm)] == \
+            [bin(v).count("1") for v in vals]
+    # a single transposition (2 5) swaps exactly bits 2 and 5
+    perm = [0, 1, 5, 3, 4, 2, 6, 7]
+    out = O.scramble(vals, perm)
+    for v, w in zip(vals, out):
+        bv, bw = _bits(v, 8), _bits(w, 8)
+        assert bw[2] == bv[5] and bw[5] == bv[2]
+        assert all(bw[i] == bv[i] for i in range(8) if i not in (2, 5))
+
+
+def _lfsr_cfg(n, rng_ids, scrambles, pool):
+    return {"rng_pool": pool,
+            "sng": {"q": [{"rng_id": r, "scramble": s} for r, s in zip(rng_ids, scrambles)],
+                    "k": [{"rng_id": rng_ids[0], "scramble": None}] * n}}
+
+
+def test_sng_shared_rng_branch():
+    """SNGBank.get_all_sequences with one shared RNG (sng.py:205-222): no scrambles ->
+    the base sequence in every row; some scrambles -> apply_scramble_batch, where None is
+    the identity over sc_prec bits, i.e. the base sequence again."""
+    pool = [{"type": "lfsr", "seed": 45, "taps": [7, 5, 4, 3]}]
+    base = O.lfsr_sequence(8, 45, [7, 5, 4, 3], 256)
+    rev = list(range(7, -1, -1))
+    cfg = _lfsr_cfg(3, [0, 0, 0], [None, None, None], pool)
+    np.testing.assert_array_equal(O.sng_sequences(cfg, "q", 8), np.stack([base] * 3))
+    cfg = _lfsr_cfg(3, [0, 0, 0], [None, rev, None], pool)
+    seqs = O.sng_sequences(cfg, "q", 8)
+    np.testing.assert_array_equal(seqs[0], base)
+    np.testing.assert_array_equal(seqs[2], base)
+    assert seqs[1].tolist() == [int(f"{v:08b}"[::-1], 2) for v in base]
+
+
+def test_sng_multi_rng_branch():
+    """Several RNG ids (sng.py:223-230): each row is its own RNG's sequence, scrambled by
+    its own permutation where one is given and raw otherwise."""
+    pool = [{"type": "lfsr", "seed": 45, "taps": [7, 5, 4, 3]},
+            {"type": "lfsr", "seed": 3, "taps": [7, 6, 5, 0]}]
+    b0 = O.lfsr_sequence(8, 45, [7, 5, 4, 3], 256)
+    b1 = O.lfsr_sequence(8, 3, [7, 6, 5, 0], 256)
+    assert not np.array_equal(b0, b1)
+    rev = list(range(7, -1, -1))
+    cfg = _lfsr_cfg(4, [0, 1, 1, 0], [None, None, rev, rev], pool)
+    seqs = O.sng_sequences(cfg, "q", 8)
+    np.testing.assert_array_equal(seqs[0], b0)
+    np.testing.assert_array_equal(seqs[1], b1)
+    assert seqs[2].tolist() == [int(f"{v:08b}"[::-1], 2) for v in b1]
+    assert seqs[3].tolist() == [int(f"{v:08b}"[::-1], 2) for v in b0]
+
+
 # ------------------------------------------------------------ prefix / Owen / rescale
 
 def test_owen_bitrev_masks():
