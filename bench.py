@@ -12,9 +12,13 @@ sc_matmul call (quantize a, quantize b, SC GEMM, epilogue).
 
 Printed: one JSON line. ``value`` is SC bit-ops/s = N*M*D*stoc_len / step time (the
 reference's unit of work; the MFMA kernel executes its own, smaller op count, reported in
-``roofline``). ``roofline`` times the dominant kernel (the SC GEMM: FP4 e2m1 MFMA by
-default, int8 MFMA or VALU popcount with --impl) with HIP events on the stream it runs on. ``cpu_baseline`` times the CPU oracle on a row sample of the same
-workload and checks those rows bit-exactly against the GPU result.
+``roofline``). After the timed steps the same number of steps runs again with HIP events
+recorded on the launch stream around every library call (the library's launch observer):
+``roofline`` is the SC GEMM launches of a step (FP4 e2m1 MFMA by default, int8 MFMA or VALU
+popcount with --impl), ``quantizers`` the quantizer launches. ``cpu_baseline`` times the
+CPU oracle on a sample of the same workload and checks those outputs bit-exactly against
+the GPU result; ``reference_cpu`` is the reference's own cfg1 call timed under
+TRITON_INTERPRET=1 in the build container (the reference does not exist on the GPU box).
 """
 from __future__ import annotations
 
@@ -97,61 +101,121 @@ def time_steps(fn, steps, warmup):
     return (time.perf_counter() - t0) / steps, out
 
 
-def gemm_event_time(run, reps):
-    """Average duration of one launch of the dominant kernel, HIP events on the current
-    stream (the stream the library launches on)."""
-    import torch
-    s = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(reps)]
-    run()
-    torch.cuda.synchronize()
-    for e0, e1 in ev:
-        e0.record(s)
-        run()
-        e1.record(s)
-    torch.cuda.synchronize()
-    ms = [e0.elapsed_time(e1) for e0, e1 in ev]
-    return float(np.mean(ms)), float(np.min(ms))
-
-
 # arithmetic the SC GEMM computes in: every kernel counts integers exactly
 DTYPE = {0: "int8 MFMA (exact int32 counts)", 1: "u32 popcount (exact int32 counts)",
          2: "e2m1 MFMA (exact integer counts in fp32)"}
 
 
-def resolve_impl(name, tabs):
-    """The kernel id the library runs for --impl `name` (auto follows sc/kernels.py)."""
-    from scmp_kernels_amd import _lib
-    if name == "valu":
-        return _lib.GEMM_VALU
-    if name == "int8":
-        return _lib.GEMM_MFMA
-    has4 = tabs.lut4(_lib.stream_of(tabs.lut.device)) is not None
-    if name == "fp4" and not has4:
-        raise SystemExit("--impl fp4: the stream table has counts e2m1 cannot represent")
-    return _lib.GEMM_MFMA_FP4 if has4 else _lib.GEMM_MFMA
-
-
-def kernel_roofline(impl, N, M, D, JP):
-    """(ops per launch, peak in 1e12/s, unit, bound, kernel name) for the SC GEMM kernel.
-    The MFMA kernels issue one multiply-add per (n, m, d, interval) over the padded interval
-    extent (JP for int8, max(JP, 32) for FP4); the VALU kernel an AND and a popcount per
-    32-interval word and bit plane."""
+def kernel_roofline(impl, N, M, D, JP, batch=1):
+    """(ops per launch, peak in 1e12/s, unit, bound, kernel name) for the SC GEMM kernel on
+    an N x M x D problem (times batch): the algorithmic work of the interval formulation
+    over the useful (unpadded) outputs. FP4 MFMA: one multiply-add per (n, m, d, interval)
+    over JPF = max(JP, 16) intervals; int8 MFMA: over JP intervals; VALU: an AND and a
+    popcount per 32-interval word and bit plane."""
+    units = float(N) * M * D * batch
     if impl == 2:
-        return (2.0 * N * M * D * max(JP, 32), MFMA_FP4_PEAK_TFLOPS, "TFLOP/s", "mfma",
+        return (2.0 * units * max(JP, 16), MFMA_FP4_PEAK_TFLOPS, "TFLOP/s", "mfma",
                 "sc_gemm_fp4_kernel")
     if impl == 0:
-        return (2.0 * N * M * D * JP, MFMA_INT8_PEAK_TOPS, "TOP/s", "mfma",
+        return (2.0 * units * JP, MFMA_INT8_PEAK_TOPS, "TOP/s", "mfma",
                 "sc_gemm_mfma_kernel")
-    return (float(N * M * D * max(1, JP // 32) * 2 * 2), VALU_PEAK_TOPS, "TOP/s", "valu",
+    return (units * max(1, JP // 32) * 2 * 2, VALU_PEAK_TOPS, "TOP/s", "valu",
             "sc_gemm_valu_kernel")
+
+
+class LaunchTimer:
+    """HIP events recorded on the launch stream (torch's current stream, which the library
+    launches on) right before and after every scmp_quantize / scmp_sc_gemm call, through
+    the library's launch observer. An FP4 GEMM call also launches a counter clear of a few
+    hundred bytes before the GEMM kernel; its time is inside the bracket."""
+
+    def __init__(self):
+        self.recs, self.pending = [], None
+
+    def __call__(self, stage, kind, info):
+        import torch
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(torch.cuda.current_stream())
+        if stage == "pre":
+            self.pending = (kind, info, ev)
+        else:
+            k, i, e0 = self.pending
+            self.recs.append((k, dict(i), e0, ev))
+
+    def durations(self):
+        import torch
+        torch.cuda.synchronize()
+        return [(k, i, e0.elapsed_time(e1)) for k, i, e0, e1 in self.recs]
+
+
+def observe_steps(fn, steps):
+    """Run `steps` more steps with the launch observer on; per-launch (kind, info, ms)."""
+    from scmp_kernels_amd.sc import kernels as K
+    timer = LaunchTimer()
+    K.launch_observer = timer
+    try:
+        for _ in range(steps):
+            fn()
+    finally:
+        K.launch_observer = None
+    return timer.durations()
+
+
+def launch_roofline(launches, steps, traffic_file=None):
+    """roofline object for the GEMM launches of the observed steps: algorithmic work of
+    all GEMM launches of a step over their summed event time (one launch per step at cfg2,
+    cfg4 two GEMMs, cfg3 a main and a tail launch, cfg5 one per level), plus one entry per
+    distinct launch; and the quantizer launches' HBM rate."""
+    gem = [(i, ms) for k, i, ms in launches if k == "sc_gemm"]
+    per = {}
+    for i, ms in gem:
+        key = (i["N"], i["M"], i["D"], i["batch"], i["JP"], i["impl"], i["chunk"])
+        per.setdefault(key, []).append(ms)
+    entries, ops_step, ms_step = [], 0.0, 0.0
+    peak = unit = bound = None
+    kernels = set()
+    for (N, M, D, batch, JP, impl, chunk), ms in per.items():
+        ops, peak, unit, bound, kname = kernel_roofline(impl, N, M, D, JP, batch)
+        kernels.add(kname)
+        avg = float(np.mean(ms))
+        ops_step += ops * len(ms) / steps
+        ms_step += float(np.sum(ms)) / steps
+        entries.append({"kernel": kname, "N": N, "M": M, "D": D, "batch": batch, "JP": JP,
+                        "chunk": chunk, "launches": len(ms), "avg_ms": round(avg, 4),
+                        "ops_per_launch": ops,
+                        "frac": round(ops / (avg * 1e-3) / 1e12 / peak, 4)})
+    achieved = ops_step / (ms_step * 1e-3) / 1e12
+    roof = {"bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": None,
+            "kernel": "+".join(sorted(kernels)), "avg_ms": round(ms_step, 4),
+            "ops_per_launch": ops_step, "launches": entries,
+            "timing": f"HIP events around every SC GEMM call of {steps} steps"}
+    if traffic_file and len(kernels) == 1:
+        tp = os.path.join(ROOT, "profiles", traffic_file)
+        if os.path.exists(tp):
+            with open(tp) as f:
+                roof["traffic"] = json.load(f).get(next(iter(kernels)), {}).get(
+                    "traffic_bytes")
+    quants = []
+    qper = {}
+    for k, i, ms in launches:
+        if k == "quantize":
+            key = (i["rows"], i["cols"], i["code_bytes"], i["variant"])
+            qper.setdefault(key, []).append(ms)
+    for (rows, cols, cbytes, var), ms in qper.items():
+        avg = float(np.mean(ms))
+        nbytes = 4 * rows * cols + cbytes
+        quants.append({"rows": rows, "cols": cols, "launches": len(ms),
+                       "avg_us": round(avg * 1e3, 2), "bytes": nbytes,
+                       "GB/s": round(nbytes / (avg * 1e-3) / 1e9, 1),
+                       "frac_of_8TB/s": round(nbytes / (avg * 1e-3) / 8e12, 3)})
+    return roof, {"bound": "hbm", "peak_GB/s": 8000.0,
+                  "bytes": "fp32 input read once + GEMM code bytes written", "launches": quants}
 
 
 def bench_cfg2(args):
     import torch
-    from scmp_kernels_amd import sc_matmul, _lib
-    from scmp_kernels_amd.sc import kernels as K
+    from scmp_kernels_amd import sc_matmul
     from scmp_kernels_amd.quant import accumulate_act_scales, compute_smooth_scales
 
     dev = torch.device("cuda", 0)
@@ -172,56 +236,15 @@ def bench_cfg2(args):
 
     t_step, y = time_steps(step, args.steps, args.warmup)
     log(f"sc_matmul step: {t_step * 1e3:.3f} ms")
-
-    # dominant kernel alone: the SC GEMM on pre-quantized codes, int32 output
-    tabs = K._get_tables(None, 8, L, 256, True, D, dev)
-    ca, cb = K._codes(N, D, dev), K._codes(M, D, dev)
-    K.quantize(a, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_DIV, code=ca,
-               code_kind=_lib.CODE_THERMO, jtab=tabs.jtab)
-    K.quantize(b, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_MUL, code=cb,
-               code_kind=_lib.CODE_Q)
-    I = torch.empty((N, M), dtype=torch.int32, device=dev)
-    epi = _lib.Epilogue()
-    epi.kind = _lib.EPI_INT
-    impl = resolve_impl(args.impl, tabs)
-
-    def gemm():
-        K.sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, iout=I, impl=impl)
-
-    g_avg, g_min = gemm_event_time(gemm, max(3, args.steps))
-
-    # the two quantizer launches of a step, each timed alone: algorithmic HBM bytes =
-    # fp32 input read once + GEMM code bytes written (padded rows) + the smoothing vector
-    def quant_a():
-        K.quantize(a, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_DIV,
-                   code=ca, code_kind=_lib.CODE_THERMO, jtab=tabs.jtab)
-
-    def quant_b():
-        K.quantize(b, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_MUL,
-                   code=cb, code_kind=_lib.CODE_Q)
-
-    quants = {}
-    for name, fn, x, c in (("a", quant_a, a, ca), ("b", quant_b, b, cb)):
-        q_avg, _ = gemm_event_time(fn, max(5, args.steps))
-        nbytes = 4 * x.numel() + c.numel() + 4 * D
-        quants[name] = {"shape": list(x.shape), "avg_us": round(q_avg * 1e3, 2),
-                        "bytes": nbytes, "GB/s": round(nbytes / (q_avg * 1e-3) / 1e9, 1),
-                        "frac_of_8TB/s": round(nbytes / (q_avg * 1e-3) / 8e12, 3)}
-    log(f"quantizers: {quants}")
-    log(f"SC GEMM kernel: avg {g_avg:.3f} ms, min {g_min:.3f} ms (JP={tabs.JP})")
+    # the same steps again with events around each launch: the GEMM launch the step runs
+    # (fused fp32 row/column epilogue) and the two quantizer launches
+    launches = observe_steps(step, max(3, args.steps))
+    roof, quants = launch_roofline(launches, max(3, args.steps), "cfg2_gemm_traffic.json")
     B = N * M * D * L
-    ops, peak, unit, bound, kname = kernel_roofline(impl, N, M, D, tabs.JP)
-    achieved = ops / (g_avg * 1e-3) / 1e12
-    roof = {
-        "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
-        "frac": round(achieved / peak, 4), "traffic": None,
-        "kernel": kname, "avg_ms": round(g_avg, 4), "ops_per_launch": ops,
-        "effective_sc_bitops_per_s": B / (g_avg * 1e-3),
-    }
-    tp = os.path.join(ROOT, "profiles", "cfg2_gemm_traffic.json")
-    if os.path.exists(tp):
-        with open(tp) as f:
-            roof["traffic"] = json.load(f).get(kname, {}).get("traffic_bytes")
+    roof["effective_sc_bitops_per_s"] = B / (roof["avg_ms"] * 1e-3)
+    log(f"SC GEMM: {roof['avg_ms']:.3f} ms per launch, {roof['frac']:.3f} of peak; "
+        f"quantizers {[q['avg_us'] for q in quants['launches']]} us")
+    impl = next(i["impl"] for k, i, _ in launches if k == "sc_gemm")
 
     cpu = None
     if not args.no_cpu:
@@ -236,16 +259,32 @@ def bench_cfg2(args):
         "dtype": DTYPE[impl], "data": "synthetic (numpy PCG64 seeds 1,2,3)",
         "config": {"workload": "cfg2: LLM linear per_row bipolar + SmoothQuant",
                    "a": [N, D], "b": [M, D], "sc_prec": 8, "stoc_len": L,
-                   "granularity": "per_row", "gemm_kernel": kname},
+                   "granularity": "per_row", "gemm_kernel": roof["kernel"]},
         "roofline": roof,
-        "quantizers": {"bound": "hbm", "peak_GB/s": 8000.0, **quants},
+        "quantizers": quants,
         "cpu_baseline": cpu,
+        "reference_cpu": reference_cpu_record(),
     }
+
+
+def reference_cpu_record():
+    """The reference's own cfg1 call timed under TRITON_INTERPRET=1 in the build container
+    (tests/golden/gen_golden.py --time-cfg1; the reference is not present on the GPU box),
+    read from the committed record."""
+    p = os.path.join(ROOT, "tests", "golden", "ref_cpu_timing.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        r = json.load(f)
+    return {"value": r["warm_sc_bitops_per_s"], "unit": "SC bit-ops/s", "cores": r["cores"],
+            "kind": "reference", "sample": r["what"] + f"; warm median {r['warm_median_s']} s"
+            f", cold {r['cold_s']} s; {r['host']['cpu']}, measured in the build container"}
 
 
 def bench_other(args):
     """The other BASELINE configurations, timed as whole calls (inputs resident in HBM,
-    tables cached after the warmup); not the driver's headline metric."""
+    tables cached after the warmup), with the GEMM launches' roofline and a CPU oracle
+    sample checked bit-exactly against the GPU result."""
     import torch
     from scmp_kernels_amd import sc_matmul
     from scmp_kernels_amd.mp import classify_rows_by_metric
@@ -261,6 +300,14 @@ def bench_other(args):
 
         def step():
             return sc_matmul(a, b, "per_row", sc_prec=8, chunk_d=72)
+
+        def cpu(y):
+            rows = np.linspace(0, N - 1, min(N, 4 * args.cpu_rows)).astype(np.int64)
+            return _cpu_sample(
+                lambda O, ctx: O.sc_matmul(a_h[rows], b_h, "per_row", sc_prec=8, chunk_d=72,
+                                           ctx=ctx),
+                lambda: y[torch.from_numpy(rows).to(dev)], len(rows) * M * D * 256,
+                f"{len(rows)} of {N} rows of a (evenly spaced) x all {M} rows of b, D={D}")
     elif args.config == "cfg4":
         q_h, k_h, p_h, vt_h = make_cfg4()
         q, k, p, vt = T(q_h), T(k_h), T(p_h), T(vt_h)
@@ -268,8 +315,20 @@ def bench_other(args):
         desc = "attention per_head bipolar BH=768: QK^T (197x197x64) + P.V (197x64x197)"
 
         def step():
-            sc_matmul(q, k, "per_head", sc_prec=8)
-            return sc_matmul(p, vt, "per_head", sc_prec=8)
+            y1 = sc_matmul(q, k, "per_head", sc_prec=8)
+            return y1, sc_matmul(p, vt, "per_head", sc_prec=8)
+
+        def cpu(y):
+            hd = np.linspace(0, 767, 384).astype(np.int64)
+            hi = torch.from_numpy(hd).to(dev)
+
+            def run(O, ctx):
+                return np.concatenate([
+                    O.sc_matmul(q_h[hd], k_h[hd], "per_head", sc_prec=8, ctx=ctx).ravel(),
+                    O.sc_matmul(p_h[hd], vt_h[hd], "per_head", sc_prec=8, ctx=ctx).ravel()])
+            return _cpu_sample(run, lambda: torch.cat([y[0][hi].ravel(), y[1][hi].ravel()]),
+                               2 * len(hd) * 197 * 197 * 64 * 256,
+                               f"{len(hd)} of 768 heads (evenly spaced), QK^T and P.V")
     elif args.config == "cfg5":
         a_h, b_h = make_cfg5()
         a, b = T(a_h), T(b_h)
@@ -283,52 +342,84 @@ def bench_other(args):
             # Y[rows_L] = sc_matmul(a[rows_L], b, stoc_len=L, rng_levels=L) for every level,
             # in one call (b quantized once per call, rows read and written in place)
             return sc_matmul_mixed(a, b, ra, mode="unipolar", group_a=4, group_b=4)
+
+        def cpu(y):
+            sel, work = [], 0
+            for L in CFG5_LEVELS:
+                rows = ra.level_row_indices[L].cpu().numpy()
+                g = np.linspace(0, len(rows) // 4 - 1, 16).astype(np.int64)
+                for gi in g:
+                    sel.append((L, rows[4 * gi:4 * gi + 4]))
+                    work += 4 * 4096 * 4096 * L
+
+            def run(O, ctx):
+                return np.concatenate([
+                    O.sc_matmul(a_h[r], b_h, "per_row", mode="unipolar", group_a=4,
+                                group_b=4, stoc_len=L, rng_levels=L, ctx=ctx).ravel()
+                    for L, r in sel])
+
+            def got():
+                return torch.cat([y[torch.from_numpy(r).to(dev)].ravel() for _, r in sel])
+            return _cpu_sample(run, got, work, "16 groups of 4 rows per level (evenly "
+                               "spaced in each level's row order) x all 4096 rows of b")
     else:
         raise SystemExit(f"unknown --config {args.config}")
-    t, _ = time_steps(step, args.steps, args.warmup)
+    t, y = time_steps(step, args.steps, args.warmup)
     log(f"{args.config}: {t * 1e3:.3f} ms per call")
+    launches = observe_steps(step, max(3, args.steps))
+    roof, quants = launch_roofline(launches, max(3, args.steps),
+                                   f"{args.config}_gemm_traffic.json")
+    log(f"{args.config} GEMMs: {roof['avg_ms']:.3f} ms per step, {roof['frac']:.3f} of peak")
+    impl = next(i["impl"] for k, i, _ in launches if k == "sc_gemm")
     return {"metric": f"ms & SC bit-ops/s per call ({desc})", "value": B / t,
             "unit": "SC bit-ops/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(t * 1e3, 4), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "data": "synthetic (numpy PCG64, bench.py generators)",
-            "config": {"workload": args.config, "sc_bit_ops": B}}
+            "vs_baseline": None, "dtype": DTYPE[impl],
+            "data": "synthetic (numpy PCG64, bench.py generators)",
+            "config": {"workload": args.config, "sc_bit_ops": B},
+            "roofline": roof, "quantizers": quants,
+            "cpu_baseline": None if args.no_cpu else cpu(y)}
+
+
+def _cpu_sample(run, got, work, sample):
+    """Time the CPU oracle on a sample (run(O, ctx) -> flat array) and compare it bit for
+    bit with the GPU's values for the same outputs (got() -> flat device tensor)."""
+    from oracle import sc_oracle as O
+    nthreads = min(16, os.cpu_count() or 1)
+    O.lib()
+    t0 = time.perf_counter()
+    ref = run(O, O.Ctx(nthreads=nthreads))
+    dt = time.perf_counter() - t0
+    g = got().cpu().numpy()
+    exact = bool(np.array_equal(g.view(np.uint32), ref.view(np.uint32)))
+    log(f"cpu oracle: {dt:.1f}s on {nthreads} threads; bit-exact={exact}")
+    return {"value": work / dt, "unit": "SC bit-ops/s", "cores": nthreads, "kind": "port",
+            "sample": f"{sample}; {dt:.1f} s", "sample_bit_exact_vs_gpu": exact}
 
 
 def profile_gemm(args):
-    """One launch of the dominant kernel on the cfg2 operands, then one device copy of a
-    known size (8 * 2^27 bytes each way) whose FETCH_SIZE / WRITE_SIZE counter values scale
-    the GEMM's counters to bytes. Used under rocprofv3 --pmc."""
+    """Two cfg2 steps (the first builds the tables), then one device copy of a known size
+    (2^28 int32 each way) whose FETCH_SIZE / WRITE_SIZE counter values scale the second
+    step's GEMM counters to bytes. Used under rocprofv3 --pmc."""
     import torch
-    from scmp_kernels_amd import _lib
-    from scmp_kernels_amd.sc import kernels as K
+    from scmp_kernels_amd import sc_matmul
     from scmp_kernels_amd.quant import accumulate_act_scales, compute_smooth_scales
     dev = torch.device("cuda", 0)
     a_h, b_h = make_cfg2()
     a = torch.from_numpy(a_h).to(dev)
     b = torch.from_numpy(b_h).to(dev)
     s = compute_smooth_scales(accumulate_act_scales(a), b, alpha=0.5)
-    N, D = a.shape
-    M = b.shape[0]
-    tabs = K._get_tables(None, 8, 256, 256, True, D, dev)
-    ca, cb = K._codes(N, D, dev), K._codes(M, D, dev)
-    K.quantize(a, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_DIV, code=ca,
-               code_kind=_lib.CODE_THERMO, jtab=tabs.jtab)
-    K.quantize(b, _lib.Q_GROUP_SYM, 127, 256, smooth=s, smooth_mode=_lib.SMOOTH_MUL, code=cb,
-               code_kind=_lib.CODE_Q)
-    I = torch.empty((N, M), dtype=torch.int32, device=dev)
-    epi = _lib.Epilogue()
-    epi.kind = _lib.EPI_INT
-    impl = resolve_impl(args.impl, tabs)
-    torch.cuda.synchronize()
-    K.sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, iout=I, impl=impl,
-              tile=args.tile)
-    torch.cuda.synchronize()
+    if args.impl != "auto":
+        os.environ["SCMP_GEMM_IMPL"] = args.impl
+    for _ in range(2):
+        sc_matmul(a, b, "per_row", sc_prec=8, stoc_len=256, smooth_scales=s)
+        torch.cuda.synchronize()
     src = torch.ones(2 ** 28, dtype=torch.int32, device=dev)     # 1 GiB
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
-    log("profile_gemm: one GEMM launch, then a 1 GiB device copy")
+    log("profile_gemm: two sc_matmul steps, then a 1 GiB device copy")
 
 
 def cpu_baseline(a_h, b_h, s_h, y_gpu, rows):
@@ -367,9 +458,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--mode", default="step", choices=["step", "gemm"],
-                    help="step: the benchmark (default); gemm: one dominant-kernel launch "
-                         "plus a 1 GiB copy, for counter collection")
-    ap.add_argument("--tile", type=int, default=0)
+                    help="step: the benchmark (default); gemm: two cfg2 steps plus a 1 GiB "
+                         "copy, for counter collection")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build runs the SC matmul on a single "

@@ -30,7 +30,8 @@ extern "C" {
 #define SCMP_E_UNSUPPORTED (-3)
 
 /* Library identification and the last error message of the calling thread. Version 2:
- * scmp_quant_args.row_index, scmp_gemm_args.row_map and scmp_gemm_args.group_class. */
+ * scmp_quant_args.row_index, scmp_gemm_args.row_map and scmp_gemm_args.group_class;
+ * version 3: scmp_quant_args.given_absmax. */
 int scmp_abi_version(void);
 const char *scmp_last_error(void);
 
@@ -162,6 +163,11 @@ typedef struct scmp_quant_args {
     /* input row of each quantized row: row r reads x row row_index[r] (each a valid row of
      * x), so a caller quantizes a row subset in any order without gathering it; NULL: r */
     const int64_t *row_index;
+    /* symmetric row-group variants (GROUP_SYM, ROW_SYM, HEAD_SYM) without column segments:
+     * max|x| of each row group given by the caller, one fp32 per group (non-negative), used
+     * in place of the reduction over x (the reference's _sc_matmul_per_head_bipolar takes
+     * its per-head ranges as arguments, scmp_kernels/sc/kernels.py:440-495); NULL: reduced */
+    const float *given_absmax;
 } scmp_quant_args;
 
 int64_t scmp_quant_workspace_bytes(int64_t rows, int64_t cols, int64_t group, int64_t seg);

@@ -674,18 +674,22 @@ def _per_row_chunked(a, b, sc_prec, L, R, chunk_d, config, ctx, parts):
     return out
 
 
-def _per_head(a, b, sc_prec, L, R, config, ctx, parts):
+def _per_head(a, b, sc_prec, L, R, config, ctx, parts, ranges=None):
     """per_head dispatch (scmp_kernels/sc/matmul.py:264-279) + _sc_matmul_per_head_bipolar
-    (scmp_kernels/sc/kernels.py:440-585)."""
+    (scmp_kernels/sc/kernels.py:440-585). ranges: the caller's per-head (q_maxs, q_mins,
+    k_maxs, k_mins), float32 (BH,) each; None: the heads' own max / min (matmul.py:271-274)."""
     BH, N, D = a.shape
     M = b.shape[1]
     if config is None:
         config = make_sobol_simple_config(D, D, sc_prec)
     Q = 2 ** (sc_prec - 1) - 1
-    amax = a.reshape(BH, -1).max(axis=1)
-    amin = a.reshape(BH, -1).min(axis=1)
-    bmax = b.reshape(BH, -1).max(axis=1)
-    bmin = b.reshape(BH, -1).min(axis=1)
+    if ranges is None:
+        amax = a.reshape(BH, -1).max(axis=1)
+        amin = a.reshape(BH, -1).min(axis=1)
+        bmax = b.reshape(BH, -1).max(axis=1)
+        bmin = b.reshape(BH, -1).min(axis=1)
+    else:
+        amax, amin, bmax, bmin = (np.asarray(r, dtype=f32).reshape(BH) for r in ranges)
     eps = f32(1e-5)
     Aq = np.maximum(np.maximum(np.abs(amax), np.abs(amin)), eps).astype(f32)
     Ak = np.maximum(np.maximum(np.abs(bmax), np.abs(bmin)), eps).astype(f32)
@@ -710,6 +714,71 @@ def _per_head(a, b, sc_prec, L, R, config, ctx, parts):
 # -------------------------------------------------------------------------------------
 # Mixed-precision row classifier (scmp_kernels/mp/config.py:154-191)
 # -------------------------------------------------------------------------------------
+
+def sc_matmul_per_tensor(a, b, max_fp_a, min_fp_a, max_fp_b=None, min_fp_b=None,
+                         mode="bipolar", sc_prec=8, config=None, stoc_len=None,
+                         rng_levels=None, ctx: Ctx = None):
+    """_sc_matmul_per_tensor with the caller's ranges, scmp_kernels/sc/kernels.py:1054-1153
+    (b's range defaults to a's, :1090-1093; 3-D runs every batch with the same ranges,
+    :1207-1226)."""
+    ctx = ctx or Ctx()
+    a, b = _c32(a), _c32(b)
+    L = stoc_len if stoc_len is not None else 2 ** sc_prec
+    R = rng_levels if rng_levels is not None else 2 ** sc_prec
+    if max_fp_b is None:
+        max_fp_b = max_fp_a
+    if min_fp_b is None:
+        min_fp_b = min_fp_a
+    rng = (float(max_fp_a), float(min_fp_a), float(max_fp_b), float(min_fp_b))
+    if a.ndim == 3:
+        return np.stack([_per_tensor_2d(a[i], b[i], *rng, mode, sc_prec, L, R, config, ctx,
+                                        {}) for i in range(a.shape[0])])
+    return _per_tensor_2d(a, b, *rng, mode, sc_prec, L, R, config, ctx, {})
+
+
+def sc_matmul_per_head_bipolar(q, k, q_maxs, q_mins, k_maxs, k_mins, sc_prec, config,
+                               stoc_len=None, rng_levels=None, ctx: Ctx = None):
+    """_sc_matmul_per_head_bipolar with the caller's per-head ranges,
+    scmp_kernels/sc/kernels.py:440-585."""
+    ctx = ctx or Ctx()
+    L = stoc_len if stoc_len is not None else 2 ** sc_prec
+    R = rng_levels if rng_levels is not None else 2 ** sc_prec
+    return _per_head(_c32(q), _c32(k), sc_prec, L, R, config, ctx, {},
+                     ranges=(q_maxs, q_mins, k_maxs, k_mins))
+
+
+def sc_matmul_per_row_mlp(a, b, max_fp_a=0.0, min_fp_a=0.0, max_fp_b=None, min_fp_b=None,
+                          mode="bipolar", sc_prec=8, config=None, group_a=1, group_b=1,
+                          chunk_d=0, stoc_len=None, rng_levels=None, ctx: Ctx = None):
+    """_sc_matmul_per_row_mlp, scmp_kernels/sc/kernels.py:1444-1566: bipolar with
+    chunk_d < D takes the chunked path (:1499-1521); other bipolar calls the row-group path
+    (:1548-1553, = _sc_matmul_per_row's, :1683-1686, :1718); unipolar quantizes per tensor
+    with the caller's ranges (:1555-1559, 1386-1418, = _sc_matmul_per_tensor's). 3-D runs
+    each batch with the ranges and without groups or chunks (:1421-1441)."""
+    ctx = ctx or Ctx()
+    a, b = _c32(a), _c32(b)
+    L = stoc_len if stoc_len is not None else 2 ** sc_prec
+    R = rng_levels if rng_levels is not None else 2 ** sc_prec
+    if max_fp_b is None:
+        max_fp_b = max_fp_a
+    if min_fp_b is None:
+        min_fp_b = min_fp_a
+    if a.ndim == 3:
+        return np.stack([sc_matmul_per_row_mlp(a[i], b[i], max_fp_a, min_fp_a, max_fp_b,
+                                               min_fp_b, mode, sc_prec, config,
+                                               stoc_len=stoc_len, rng_levels=rng_levels,
+                                               ctx=ctx) for i in range(a.shape[0])])
+    D = a.shape[1]
+    if mode == "bipolar" and chunk_d > 0 and D > chunk_d:
+        return _per_row_chunked(a, b, sc_prec, L, R, chunk_d, config, ctx, {})
+    if mode == "bipolar":
+        return _per_row_2d(a, b, max(group_a, 1), max(group_b, 1), mode, sc_prec, L, R,
+                           config, ctx, {})
+    if mode != "unipolar":
+        raise ValueError(f"Unknown mode: {mode}")
+    return _per_tensor_2d(a, b, float(max_fp_a), float(min_fp_a), float(max_fp_b),
+                          float(min_fp_b), mode, sc_prec, L, R, config, ctx, {})
+
 
 def classify_rows_by_metric(metric: np.ndarray, levels: list, fractions: list):
     """Rank rows by metric (descending, stable like torch's argsort on CPU is NOT

@@ -43,7 +43,7 @@ class QuantArgs(ctypes.Structure):
         ("beta16", c_vp), ("beta32", c_vp), ("beta_formula", c_int), ("sign", c_vp),
         ("xint", c_vp), ("out_ld", c_i64), ("scale", c_vp), ("scale64", c_vp), ("inv", c_vp),
         ("zp", c_vp), ("zp64", c_vp), ("rowsum", c_vp), ("workspace", c_vp),
-        ("row_index", c_vp),
+        ("row_index", c_vp), ("given_absmax", c_vp),
     ]
 
 

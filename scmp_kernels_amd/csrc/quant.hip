@@ -51,6 +51,14 @@ __global__ void stats_init_kernel(uint32_t *stats, int64_t n) {
     if (i < n) stats[i] = 0u;
 }
 
+// stats of each (row group) from the caller's max|x| (symmetric variants, one segment)
+__global__ void stats_given_kernel(uint32_t *stats, const float *given, int64_t nunits) {
+    int64_t u = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (u >= nunits) return;
+    stats[u * 2 + 0] = __float_as_uint(fabsf(given[u]));
+    stats[u * 2 + 1] = 0u;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
@@ -984,13 +992,24 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
 
     const bool host = a.variant == SCMP_Q_HOST_SYM || a.variant == SCMP_Q_HOST_ASYM;
     const bool tensor = a.variant == SCMP_Q_TENSOR_SYM || a.variant == SCMP_Q_TENSOR_ASYM;
-    if (!host && !tensor && nseg == 1 && G <= kGroupMaxRows && G * a.cols <= (1 << 22) &&
+    const bool given = a.given_absmax != nullptr;
+    if (given) {
+        SCMP_REQUIRE(a.variant == SCMP_Q_GROUP_SYM || a.variant == SCMP_Q_ROW_SYM ||
+                     a.variant == SCMP_Q_HEAD_SYM,
+                     "scmp_quantize: given_absmax needs a symmetric row-group variant (got %d)",
+                     a.variant);
+        SCMP_REQUIRE(nseg == 1, "scmp_quantize: given_absmax does not take column segments");
+        stats_given_kernel<<<cdiv(nunits, 256), 256, 0, stream>>>(stats, a.given_absmax,
+                                                                   nunits);
+        SCMP_LAUNCH_CHECK("scmp_quantize/given");
+    }
+    if (!given && !host && !tensor && nseg == 1 && G <= kGroupMaxRows && G * a.cols <= (1 << 22) &&
         (!a.code || a.code_ld % 4 == 0))
         return quantize_groups(a, G, stream);
-    if (!host && !tensor && nseg > 1 && G == 1 && nseg <= kMaxSegs && segw % 4 == 0 &&
+    if (!given && !host && !tensor && nseg > 1 && G == 1 && nseg <= kMaxSegs && segw % 4 == 0 &&
         a.cols <= 4 * kGroupThreads * kMaxChunks && (!a.code || a.code_ld % 4 == 0))
         return quantize_segments(a, segw, nseg, stream);
-    if (!host) {
+    if (!host && !given) {
         stats_init_kernel<<<cdiv(2 * nunits, 256), 256, 0, stream>>>(stats, 2 * nunits);
         SCMP_LAUNCH_CHECK("scmp_quantize/init");
         int64_t ntask = a.rows * nseg;

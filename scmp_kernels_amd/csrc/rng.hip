@@ -232,7 +232,7 @@ using namespace scmp;
 
 extern "C" {
 
-int scmp_abi_version(void) { return 2; }
+int scmp_abi_version(void) { return 3; }
 
 const char *scmp_last_error(void) { return g_err; }
 

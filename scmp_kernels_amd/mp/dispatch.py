@@ -23,6 +23,27 @@ from ..quant.smoothquant import _check_smoothing_vector
 from .config import RowAssignment
 
 
+def _check_rows(row_lists, N: int) -> bool:
+    """Validate the row indices the kernels will read and write, with one host sync: every
+    index in [0, N) and no row in two places (a repeated row would be written twice, by two
+    levels or by two row groups of one level, with different values). Returns whether the
+    rows cover all N rows exactly once (then the output needs no zero fill)."""
+    if not row_lists:
+        return N == 0
+    idx = torch.cat(row_lists)
+    lo, hi = torch.aminmax(idx)
+    cnt = torch.bincount(idx.clamp(0, max(N - 1, 0)), minlength=max(N, 1))
+    lo, hi, most, seen = (int(v) for v in torch.stack(
+        [lo, hi, cnt.max(), (cnt > 0).sum()]).cpu())
+    if lo < 0 or hi >= N:
+        raise ValueError(f"sc_matmul_mixed: row indices must lie in [0, {N}), got "
+                         f"[{lo}, {hi}]")
+    if most > 1:
+        raise ValueError("sc_matmul_mixed: a row appears more than once in the assignment "
+                         "(each row belongs to one level, once)")
+    return seen == N
+
+
 @torch.no_grad()
 def sc_matmul_mixed(a: torch.Tensor, b, assignment: RowAssignment, *, mode: str = "unipolar",
                     sc_prec: int = 8, group_a: int = 1, group_b: int = 1,
@@ -66,10 +87,9 @@ def sc_matmul_mixed(a: torch.Tensor, b, assignment: RowAssignment, *, mode: str 
         _check_smoothing_vector(smooth_scales, D, names=("a",))
         smooth = smooth_scales.to(device=dev, dtype=torch.float32).contiguous()
 
-    levels, pruned, covered = [], [], 0
+    levels, pruned = [], []
     for L, rows in assignment.level_row_indices.items():
         rows = rows.to(device=dev, dtype=torch.int64).contiguous()
-        covered += int(rows.numel())
         L = int(L)
         if rows.numel() == 0:
             continue
@@ -80,19 +100,12 @@ def sc_matmul_mixed(a: torch.Tensor, b, assignment: RowAssignment, *, mode: str 
             raise ValueError(f"sc_matmul: stoc_len={L} exceeds 2**sc_prec={2 ** sc_prec}; the "
                              f"RNG sequences are 2**sc_prec long.")
         levels.append((L, L if rng_levels is None else int(rng_levels), rows))
-    if levels or pruned:
-        # the row indices are read by the kernels: one bounds check per call
-        lo, hi = torch.aminmax(torch.cat([r for _, _, r in levels] + pruned))
-        lo, hi = int(lo), int(hi)
-        if lo < 0 or hi >= N:
-            raise ValueError(f"sc_matmul_mixed: row indices must lie in [0, {N}), got "
-                             f"[{lo}, {hi}]")
+    exact = _check_rows([r for _, _, r in levels] + pruned, N)
     M = b.M if prepared else b.shape[0]
     with torch.cuda.device(dev):
         if prepared:
             b.check(D, mode, sc_prec, group_b, smooth_scales)
-        y = (torch.empty if covered == N else torch.zeros)((N, M), dtype=torch.float32,
-                                                          device=dev)
+        y = (torch.empty if exact else torch.zeros)((N, M), dtype=torch.float32, device=dev)
         for rows in pruned:
             y.index_fill_(0, rows, 0.0)
         _k._per_row_levels(a, b, levels, y, group_a=group_a, group_b=group_b, mode=mode,

@@ -109,9 +109,11 @@ def quantize(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, *, grou
              code_batch_rows: int = 0, jtab=None, col_class=None, beta16=None, beta32=None,
              beta_formula: int = 0, sign=None, xint=None, scale=None, scale64=None, inv=None,
              zp=None, zp64=None, rowsum=None, host_inv: float = 0.0, host_zp: float = 0.0,
-             row_index=None):
+             row_index=None, given_absmax=None):
     """One scmp_quantize call on the current stream; outputs are written in place.
-    row_index (int64 device tensor): quantize rows x[row_index] in that order."""
+    row_index (int64 device tensor): quantize rows x[row_index] in that order.
+    given_absmax (float32 device tensor, one value per row group): the groups' max|x| from
+    the caller instead of the reduction (symmetric variants)."""
     x = _rows2d(x)
     rows, cols = x.shape
     if row_index is not None:
@@ -135,7 +137,15 @@ def quantize(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, *, grou
     ws = _workspace(rows, cols, G, seg, x.device)
     a.workspace = ws.data_ptr()
     a.row_index = _lib.ptr(row_index)
+    a.given_absmax = _lib.ptr(given_absmax)
+    info = None
+    if launch_observer is not None:
+        info = {"rows": rows, "cols": cols, "in_bytes": 4 * rows * cols,
+                "code_bytes": 0 if code is None else code.numel(), "variant": variant}
+        _observe("pre", "quantize", info)
     _lib.check(_lib.load().scmp_quantize(a, _lib.stream_of(x.device)), "scmp_quantize")
+    if info is not None:
+        _observe("post", "quantize", info)
     return ws  # keep the workspace alive until the stream has consumed it
 
 
@@ -181,6 +191,19 @@ def _permute_codes(c: torch.Tensor, src: torch.Tensor, Dp: int, stream) -> torch
     return out
 
 
+# Observer of the library's launches: when set, called as observer(stage, kind, info) with
+# stage "pre" / "post" right before and after each scmp_quantize / scmp_sc_gemm call
+# (kind "quantize" / "sc_gemm"), on the thread that issues it, so that a profiler can
+# record events on the launch stream around it. info holds the call's shape. None: off.
+launch_observer = None
+
+
+def _observe(stage, kind, info):
+    obs = launch_observer
+    if obs is not None:
+        obs(stage, kind, info)
+
+
 def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.Epilogue",
             y=None, iout=None, ldy=None, bsy=0, chunk=0, d_class=None, impl=None, tile=None,
             row_map=None):
@@ -195,7 +218,14 @@ def sc_gemm(ca, cb, *, N, M, D, batch, tabs: "_tables.StreamTables", epi: "_lib.
     if nbytes > 0:
         ws = torch.empty(nbytes, dtype=torch.uint8, device=ca.device)
         g.workspace, g.workspace_bytes = ws.data_ptr(), nbytes
+    info = None
+    if launch_observer is not None:
+        info = {"N": N, "M": M, "D": D, "batch": max(batch, 1), "JP": tabs.JP,
+                "impl": g.impl, "chunk": chunk, "epi": epi.kind}
+        _observe("pre", "sc_gemm", info)
     _lib.check(lib.scmp_sc_gemm(g, _lib.stream_of(ca.device)), "scmp_sc_gemm")
+    if info is not None:
+        _observe("post", "sc_gemm", info)
     return ws, keep  # keep the buffers alive until the stream has consumed them
 
 
@@ -481,29 +511,60 @@ def _per_row_levels(a, b, levels, y, *, group_a, group_b, mode, sc_prec, config,
 # -------------------------------------------------------------------------------------
 
 @torch.no_grad()
-def _sc_matmul_per_row_mlp(a, b, mode="bipolar", sc_prec=8, config=None, group_a=1,
-                           group_b=1, chunk_d=0, stoc_len=None, rng_levels=None,
-                           smooth_scales=None):
+def _sc_matmul_per_row_mlp(a, b, max_fp_a=0.0, min_fp_a=0.0, max_fp_b=None, min_fp_b=None,
+                           mode="bipolar", sc_prec=8, config=None, group_a=1, group_b=1,
+                           chunk_d=0, stoc_len=None, rng_levels=None, *, smooth_scales=None):
+    """scmp_kernels/sc/kernels.py:1444-1566, same parameters. Bipolar with chunk_d < D: the
+    chunked path (one launch, per-chunk scales). Other bipolar calls: the row-group path of
+    _sc_matmul_per_row (kernels.py:1548-1553; group sizes <= 0 mean 1). Unipolar: per-tensor
+    quantization with the caller's ranges (max_fp_b / min_fp_b default to a's), which is
+    _sc_matmul_per_tensor's (kernels.py:1386-1418). 3-D: each batch with the ranges and
+    without groups or chunks (kernels.py:1421-1441)."""
     if stoc_len is None:
         stoc_len = 2 ** sc_prec
+    if max_fp_b is None:
+        max_fp_b = max_fp_a
+    if min_fp_b is None:
+        min_fp_b = min_fp_a
+    if a.dim() == 3:
+        out = torch.empty((a.shape[0], a.shape[1], b.shape[1]), dtype=torch.float32,
+                          device=a.device)
+        for i in range(a.shape[0]):
+            out[i] = _sc_matmul_per_row_mlp(a[i], b[i], max_fp_a, min_fp_a, max_fp_b,
+                                            min_fp_b, mode, sc_prec, config, stoc_len=stoc_len,
+                                            rng_levels=rng_levels, smooth_scales=smooth_scales)
+        return out
     assert a.dim() == 2 and b.dim() == 2, f"Expected 2D, got a:{a.dim()}D b:{b.dim()}D"
     assert a.shape[1] == b.shape[1], f"Dim mismatch: a={a.shape[1]}, b={b.shape[1]}"
     N, D = a.shape
-    if not (mode == "bipolar" and chunk_d > 0 and D > chunk_d):
+    if mode == "unipolar":
+        return _sc_matmul_per_tensor(a, b, max_fp_a, min_fp_a, max_fp_b, min_fp_b,
+                                     mode=mode, sc_prec=sc_prec, config=config,
+                                     stoc_len=stoc_len, rng_levels=rng_levels,
+                                     smooth_scales=smooth_scales)
+    if mode != "bipolar":
+        raise ValueError(f"Unknown mode: {mode}")
+    if not (chunk_d > 0 and D > chunk_d):
         # standard path: the grouped quantizer arithmetic of _sc_matmul_per_row
-        return _sc_matmul_per_row(a, b, group_a=group_a, group_b=group_b, mode=mode,
-                                  sc_prec=sc_prec, config=config, stoc_len=stoc_len,
-                                  rng_levels=rng_levels, smooth_scales=smooth_scales)
+        return _sc_matmul_per_row(a, b, group_a=max(group_a, 1), group_b=max(group_b, 1),
+                                  mode=mode, sc_prec=sc_prec, config=config,
+                                  stoc_len=stoc_len, rng_levels=rng_levels,
+                                  smooth_scales=smooth_scales)
     a, b, home = _to_gpu(a, b)
     M = b.shape[0]
     dev = a.device
     R = _resolve_rng_levels(sc_prec, rng_levels)
     Q = 2 ** (sc_prec - 1) - 1
+    # Tables of at most 32 intervals put two inner dimensions in one MFMA k-step (both
+    # kernels), so a chunk must end on an even d; for an odd chunk_d the table is widened
+    # to 64 intervals (empty past the attainable ones: the same sums), one d per k-step.
     tabs = _tables.get_tables(config, ("sobol_simple", chunk_d, chunk_d, sc_prec),
                               lambda: make_sobol_simple_config(chunk_d, chunk_d, sc_prec),
-                              sc_prec, stoc_len, R, True, chunk_d, dev)
-    if tabs.JP == 16 and chunk_d % 2:
-        raise NotImplementedError("sc_matmul: chunk_d must be even for stoc_len <= 16")
+                              sc_prec, stoc_len, R, True, chunk_d, dev,
+                              min_jp=64 if chunk_d % 2 else 16)
+    impl = _gemm_impl()
+    if impl == _lib.GEMM_VALU:
+        impl = None                    # the VALU kernel has no chunked accumulation
     # dimension d of every chunk uses the tables of local index d mod chunk_d
     d_class = None
     if tabs.nclass > 1:
@@ -524,9 +585,8 @@ def _sc_matmul_per_row_mlp(a, b, mode="bipolar", sc_prec=8, config=None, group_a
     epi.kind, epi.c = _lib.EPI_ROWCOL, _inner_scale(Q, stoc_len)
     epi.sa, epi.sb = sa.data_ptr(), sb.data_ptr()
     epi.sa_chunk_stride, epi.sb_chunk_stride = N, M
-    impl = _gemm_impl()
     sc_gemm(ca, cb, N=N, M=M, D=D, batch=1, tabs=tabs, epi=epi, y=y, chunk=chunk_d,
-            d_class=d_class, impl=None if impl == _lib.GEMM_VALU else impl)
+            d_class=d_class, impl=impl)
     del w1, w2
     return y.to(home) if home is not None else y
 
@@ -597,9 +657,24 @@ def _sc_matmul_per_row_batched(a, b, group_a=1, group_b=1, mode="bipolar", sc_pr
 # per_head bipolar (scmp_kernels/sc/kernels.py:440-585)
 # -------------------------------------------------------------------------------------
 
+def _head_absmax(maxs, mins, BH, dev, name):
+    """max(|max|, |min|) per head (kernels.py:490-491; the 1e-5 clamp is the quantizer's)."""
+    mx = torch.as_tensor(maxs, device=dev).reshape(-1).float()
+    mn = torch.as_tensor(mins, device=dev).reshape(-1).float()
+    if mx.numel() != BH or mn.numel() != BH:
+        raise ValueError(f"_sc_matmul_per_head_bipolar: {name}_maxs / {name}_mins need one "
+                         f"value per head ({BH}), got {mx.numel()} and {mn.numel()}")
+    return torch.maximum(mx.abs(), mn.abs()).contiguous()
+
+
 @torch.no_grad()
-def _sc_matmul_per_head_bipolar(q_flat, k_flat, sc_prec, config, stoc_len=None,
-                                rng_levels=None, smooth_scales=None):
+def _sc_matmul_per_head_bipolar(q_flat, k_flat, q_maxs=None, q_mins=None, k_maxs=None,
+                                k_mins=None, sc_prec=8, config=None, stoc_len=None,
+                                rng_levels=None, *, smooth_scales=None):
+    """scmp_kernels/sc/kernels.py:440-585, same parameters: q_maxs / q_mins / k_maxs /
+    k_mins are the (BH,) per-head ranges the quantizers scale by. None (this build's
+    sc_matmul) takes each head's own max and min, reduced on the device, which is what the
+    reference's sc_matmul passes (sc/matmul.py:271-274)."""
     if stoc_len is None:
         stoc_len = 2 ** sc_prec
     BH, N, D = q_flat.shape
@@ -608,8 +683,16 @@ def _sc_matmul_per_head_bipolar(q_flat, k_flat, sc_prec, config, stoc_len=None,
         raise ValueError(
             f"_sc_matmul_per_head_bipolar: shape mismatch — q is (BH={BH}, N={N}, D={D}), "
             f"k is (BH={BH_k}, M={M}, D={D_k}); require equal BH and D.")
+    given = [r is not None for r in (q_maxs, q_mins, k_maxs, k_mins)]
+    if any(given) and not all(given):
+        raise ValueError("_sc_matmul_per_head_bipolar: give all four of q_maxs, q_mins, "
+                         "k_maxs, k_mins, or none")
     q_flat, k_flat, home = _to_gpu(q_flat, k_flat)
     dev = q_flat.device
+    gq = gk = None
+    if all(given):
+        gq = _head_absmax(q_maxs, q_mins, BH, dev, "q")
+        gk = _head_absmax(k_maxs, k_mins, BH, dev, "k")
     Q = 2 ** (sc_prec - 1) - 1
     R = _resolve_rng_levels(sc_prec, rng_levels)
     tabs = _tables.get_tables(config, ("sobol_simple", D, D, sc_prec),
@@ -622,9 +705,10 @@ def _sc_matmul_per_head_bipolar(q_flat, k_flat, sc_prec, config, stoc_len=None,
     s_b, m_b = _smooth_args(smooth_scales, "b")
     w1 = quantize(q_flat.reshape(BH * N, D), _lib.Q_HEAD_SYM, Q, R, group=N, smooth=s_a,
                   smooth_mode=m_a, code=ca, code_kind=_lib.CODE_THERMO, code_batch_rows=N,
-                  jtab=tabs.jtab, col_class=tabs.d_class, scale=sq)
+                  jtab=tabs.jtab, col_class=tabs.d_class, scale=sq, given_absmax=gq)
     w2 = quantize(k_flat.reshape(BH * M, D), _lib.Q_HEAD_SYM, Q, R, group=M, smooth=s_b,
-                  smooth_mode=m_b, code=cb, code_kind=_lib.CODE_Q, code_batch_rows=M, scale=sk)
+                  smooth_mode=m_b, code=cb, code_kind=_lib.CODE_Q, code_batch_rows=M, scale=sk,
+                  given_absmax=gk)
     # out_scale = scale_q * scale_k (kernels.py:550), fp32
     hs = (sq[::N] * sk[::M]).contiguous()
     y = torch.empty((BH, N, M), dtype=torch.float32, device=dev)
@@ -640,11 +724,40 @@ def _sc_matmul_per_head_bipolar(q_flat, k_flat, sc_prec, config, stoc_len=None,
 # per_tensor (scmp_kernels/sc/kernels.py:1054-1226), ranges reduced on the device
 # -------------------------------------------------------------------------------------
 
+def _host_scales(max_fp, min_fp, mode, Q):
+    """The reference's Python-float scale math for a caller's range: bipolar
+    (scale, 1 / scale, 0) from max(|max|, |min|, 1e-5) (kernels.py:1173-1176,
+    quant/fused.py:172-174); unipolar (scale, 1 / scale, zp) (quant/fused.py:204-209)."""
+    max_fp, min_fp = float(max_fp), float(min_fp)
+    if mode == "bipolar":
+        scale = max(abs(max_fp), abs(min_fp), 1e-5) / Q
+        return scale, 1.0 / scale, 0.0
+    scale = max(max_fp - min_fp, 1e-5) / Q
+    zp = float(max(0, min(Q, round(-min_fp / scale))))
+    return scale, 1.0 / scale, zp
+
+
 @torch.no_grad()
-def _sc_matmul_per_tensor(a, b, mode="bipolar", sc_prec=8, config=None, stoc_len=None,
-                          rng_levels=None, smooth_scales=None):
+def _sc_matmul_per_tensor(a, b, max_fp_a=None, min_fp_a=None, max_fp_b=None, min_fp_b=None,
+                          mode="bipolar", sc_prec=8, config=None, stoc_len=None,
+                          rng_levels=None, *, smooth_scales=None):
+    """scmp_kernels/sc/kernels.py:1054-1153, same parameters. Given ranges are used as the
+    reference uses them (Python-float scales; b's default to a's; a 3-D call uses them for
+    every batch). None (this build's sc_matmul) reduces the whole tensors' max and min on
+    the device, which is what the reference's sc_matmul passes (sc/matmul.py:214-225), with
+    the scale math in float64 on the device and no host sync."""
     if stoc_len is None:
         stoc_len = 2 ** sc_prec
+    if (max_fp_a is None) != (min_fp_a is None):
+        raise ValueError("_sc_matmul_per_tensor: give both max_fp_a and min_fp_a, or neither")
+    if max_fp_a is None and (max_fp_b is not None or min_fp_b is not None):
+        raise ValueError("_sc_matmul_per_tensor: b's range needs a's (max_fp_a, min_fp_a)")
+    host = max_fp_a is not None
+    if host:
+        if max_fp_b is None:
+            max_fp_b = max_fp_a
+        if min_fp_b is None:
+            min_fp_b = min_fp_a
     if a.dim() == 3:
         BH, N, D = a.shape
         M = b.shape[1]
@@ -671,7 +784,37 @@ def _sc_matmul_per_tensor(a, b, mode="bipolar", sc_prec=8, config=None, stoc_len
     sb64 = torch.empty(1, dtype=torch.float64, device=dev)
     y = torch.empty((batch, N, M) if batch else (N, M), dtype=torch.float32, device=dev)
     epi = _lib.Epilogue()
-    if bip:
+    if host:
+        Q = 2 ** (sc_prec - 1) - 1 if bip else 2 ** sc_prec - 1
+        sca, inva, zpa = _host_scales(max_fp_a, min_fp_a, mode, Q)
+        scb, invb, zpb = _host_scales(max_fp_b, min_fp_b, mode, Q)
+        var = _lib.Q_HOST_SYM if bip else _lib.Q_HOST_ASYM
+        za = zb = ra = rb = None
+        if not bip:
+            za = torch.empty(nb * N, dtype=torch.float32, device=dev)
+            zb = torch.empty(nb * M, dtype=torch.float32, device=dev)
+            ra = torch.empty(nb * N, dtype=torch.float32, device=dev)
+            rb = torch.empty(nb * M, dtype=torch.float32, device=dev)
+        w1 = quantize(a2, var, Q, R, smooth=s_a, smooth_mode=m_a, code=ca,
+                      code_kind=_lib.CODE_THERMO, code_batch_rows=N if batch else 0,
+                      jtab=tabs.jtab, col_class=tabs.d_class, host_inv=inva, host_zp=zpa,
+                      zp=za, rowsum=ra)
+        w2 = quantize(b2, var, Q, R, smooth=s_b, smooth_mode=m_b, code=cb,
+                      code_kind=_lib.CODE_Q, code_batch_rows=M if batch else 0, host_inv=invb,
+                      host_zp=zpb, zp=zb, rowsum=rb)
+        # Python-float products, rounded to fp32 where torch multiplies (kernels.py:1202-1204)
+        s = torch.tensor([sca * scb], dtype=torch.float32).to(dev)
+        epi.c, epi.s = _inner_scale(Q, stoc_len), s.data_ptr()
+        if bip:
+            epi.kind = _lib.EPI_SCALAR
+        else:
+            t3 = torch.tensor([D * zpa * zpb], dtype=torch.float32).to(dev)
+            epi.kind = _lib.EPI_ZP_SCALAR
+            epi.za, epi.zb, epi.t3 = za.data_ptr(), zb.data_ptr(), t3.data_ptr()
+            epi.suma, epi.sumb = ra.data_ptr(), rb.data_ptr()
+            epi.sa_batch_stride, epi.sb_batch_stride = N, M
+        sc_gemm(ca, cb, N=N, M=M, D=D, batch=nb, tabs=tabs, epi=epi, y=y, bsy=N * M)
+    elif bip:
         Q = 2 ** (sc_prec - 1) - 1
         w1 = quantize(a2, _lib.Q_TENSOR_SYM, Q, R, smooth=s_a, smooth_mode=m_a, code=ca,
                       code_kind=_lib.CODE_THERMO, code_batch_rows=N if batch else 0,

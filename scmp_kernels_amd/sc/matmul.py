@@ -16,6 +16,11 @@ from typing import Optional
 import torch
 
 from . import kernels as _paths
+# the per-path entry points, reachable from this module as in the reference
+# (scmp_kernels/sc/matmul.py:23-29); each takes the reference's parameter list
+from .kernels import (_sc_matmul_per_head_bipolar, _sc_matmul_per_row,  # noqa: F401
+                      _sc_matmul_per_row_batched, _sc_matmul_per_row_mlp,
+                      _sc_matmul_per_tensor)
 from ..quant.smoothquant import apply_smoothing, _check_smoothing_vector
 
 _VALID_GRANULARITIES = ("per_tensor", "per_row", "per_head")

@@ -255,10 +255,13 @@ def prepare(r: torch.Tensor, p: int, L: int, R: int, masks: Optional[np.ndarray]
 
 
 def get_tables(config: Optional[dict], default_desc: tuple, make_config, sc_prec: int,
-               L: int, R: int, bipolar: bool, D: int, device) -> StreamTables:
+               L: int, R: int, bipolar: bool, D: int, device,
+               min_jp: int = 16) -> StreamTables:
     """Cached stream tables for inner dimensions 0..D-1 of `config` (built with
-    make_config() when config is None)."""
-    key = (config_key(config, default_desc), sc_prec, L, R, bipolar, D, str(device))
+    make_config() when config is None). min_jp: table width of at least this many intervals
+    (a power of two; intervals past the attainable ones are empty, so every sum is the
+    same)."""
+    key = (config_key(config, default_desc), sc_prec, L, R, bipolar, D, str(device), min_jp)
     t = _table_cache.get(key)
     if t is not None:
         return t
@@ -284,7 +287,7 @@ def get_tables(config: Optional[dict], default_desc: tuple, make_config, sc_prec
     _, rep, class_of = np.unique(both, axis=0, return_index=True, return_inverse=True)
     class_of = class_of.reshape(-1).astype(np.int32)
     nclass = len(rep)
-    JP = interval_width(sc_prec, L, R, bipolar)
+    JP = max(interval_width(sc_prec, L, R, bipolar), min_jp)
     lib = _lib.load()
     stream = _lib.stream_of(device)
     jtab = torch.empty((nclass, 256), dtype=torch.uint8, device=device)

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = _lib.load()
-    assert lib.scmp_abi_version() == 2
+    assert lib.scmp_abi_version() == 3
     assert isinstance(lib.scmp_last_error(), bytes)
 
 

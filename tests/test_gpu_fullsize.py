@@ -81,20 +81,18 @@ def test_cfg4_attention_per_head():
 def test_cfg5_mixed_level_unipolar_grouped():
     """4096 x 4096 x 4096 unipolar, groups of 4 rows, per-row levels {256, 64, 16} from
     classify_rows_by_metric on the row range (equal fractions, descending-metric order
-    inside a level). Sampled: whole groups of 4 rows of every level."""
-    from scmp_kernels_amd import sc_matmul
-    from scmp_kernels_amd.mp import classify_rows_by_metric
+    inside a level), through the benchmarked call sc_matmul_mixed. Sampled: whole groups of
+    4 rows at the start, middle and end of every level (a level's row groups follow its row
+    order), checked against the oracle's sc_matmul of those rows at the level's length."""
+    from scmp_kernels_amd.mp import classify_rows_by_metric, sc_matmul_mixed
     a_h, b_h = bench.make_cfg5()
     a, b = _dev(a_h), _dev(b_h)
     metric = (a.amax(dim=1) - a.amin(dim=1))
     ra = classify_rows_by_metric(metric, bench.CFG5_LEVELS, [1 / 3] * 3)
-    Y = torch.empty((4096, 4096), dtype=torch.float32, device="cuda")
+    Y = sc_matmul_mixed(a, b, ra, mode="unipolar", group_a=4, group_b=4)
+    assert torch.equal(Y, sc_matmul_mixed(a, b, ra, mode="unipolar", group_a=4, group_b=4))
     for L in bench.CFG5_LEVELS:
-        rows = ra.level_row_indices[L]
-        yl = sc_matmul(a[rows], b, "per_row", mode="unipolar", group_a=4, group_b=4,
-                       stoc_len=L, rng_levels=L)
-        Y[rows] = yl
-        rows_h = rows.cpu().numpy()
+        rows_h = ra.level_row_indices[L].cpu().numpy()
         ngroups = (len(rows_h) + 3) // 4
         for g in (0, ngroups // 2, ngroups - 1):
             sel = rows_h[4 * g:4 * g + 4]
@@ -102,3 +100,22 @@ def test_cfg5_mixed_level_unipolar_grouped():
                               stoc_len=L, rng_levels=L, ctx=CTX)
             _bits_equal(Y[torch.from_numpy(sel).cuda()].cpu().numpy(), ref,
                         f"cfg5 level {L} group {g}")
+
+
+def test_cfg2_prepared_weight_smoothquant():
+    """The weight-side cache at cfg2: prepare_weight(b, smooth_scales=s) once, then
+    sc_matmul(a, w, ...) on sampled rows against the oracle's plain call (b * s folded into
+    the weight quantizer's load, a / s into the activation quantizer's)."""
+    from scmp_kernels_amd import sc_matmul
+    from scmp_kernels_amd.quant import accumulate_act_scales, compute_smooth_scales
+    from scmp_kernels_amd.sc import prepare_weight
+    a_h, b_h = bench.make_cfg2()
+    a, b = _dev(a_h), _dev(b_h)
+    s = compute_smooth_scales(accumulate_act_scales(a), b, alpha=0.5)
+    w = prepare_weight(b, mode="bipolar", sc_prec=8, smooth_scales=s)
+    del b
+    y = sc_matmul(a, w, "per_row", sc_prec=8, stoc_len=256, smooth_scales=s)
+    rows = _sample_rows(4096, 24, 23)
+    ref = O.sc_matmul(a_h[rows], b_h, "per_row", sc_prec=8, stoc_len=256,
+                      smooth_scales=s.cpu().numpy(), ctx=CTX)
+    _bits_equal(y[torch.from_numpy(rows).cuda()].cpu().numpy(), ref, "cfg2 prepared rows")

@@ -142,3 +142,30 @@ def test_mixed_rejects_bad_rows():
                        level_row_indices={256: torch.tensor([0, 3, 10])})
     with pytest.raises(ValueError, match="row indices"):
         sc_matmul_mixed(a, b, ra)
+
+
+def test_mixed_rejects_repeated_rows_and_zero_fills_missing():
+    """A row in two places is rejected (it would be written twice with different values);
+    rows that no level names are zero, also when the index count equals N."""
+    from scmp_kernels_amd.mp import RowAssignment, sc_matmul_mixed
+    dev = _dev()
+    a_h, b_h, _ = _data(12, 9, 64, 7)
+    a, b = torch.from_numpy(a_h).to(dev), torch.from_numpy(b_h).to(dev)
+    lv = torch.zeros(12, dtype=torch.long)
+    dup = RowAssignment(row_levels=lv, level_row_indices={
+        256: torch.tensor([0, 1, 2, 3, 4, 5]), 64: torch.tensor([6, 7, 8, 9, 10, 5])})
+    with pytest.raises(ValueError, match="more than once"):
+        sc_matmul_mixed(a, b, dup, mode="bipolar")
+    dup1 = RowAssignment(row_levels=lv, level_row_indices={
+        256: torch.tensor([0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 10])})
+    with pytest.raises(ValueError, match="more than once"):
+        sc_matmul_mixed(a, b, dup1, mode="bipolar")
+    part = RowAssignment(row_levels=lv, level_row_indices={
+        256: torch.tensor([0, 2, 4, 6]), 64: torch.tensor([1, 3, 5])})
+    y = sc_matmul_mixed(a, b, part, mode="bipolar")
+    assert not y[7:].any()
+    for L, rows in part.level_row_indices.items():
+        r = rows.numpy()
+        ref = O.sc_matmul(a_h[r], b_h, "per_row", mode="bipolar", sc_prec=8, stoc_len=L,
+                          rng_levels=L)
+        np.testing.assert_array_equal(y.cpu().numpy()[r].view(np.uint32), ref.view(np.uint32))

@@ -77,7 +77,7 @@ def test_prepare_prefix(L, R, mode, srs):
     else:
         np.testing.assert_array_equal(masks, ref_masks)
     got = TB.prepare(got_full, 8, L, R, masks, srs)
-    bits_equal(got, O.prepare_prefix(ref_full, 8, L, R, mode, srs))
+    bits_equal(got, O.prepare_prefix(ref_full, 8, L, R, mode, srs, owen_device=_dev()))
 
 
 def test_scrambled_config_sequences():
@@ -493,6 +493,10 @@ RANDOM_CASES = [
     # 16-interval tables through the chunk_d kernel (stored in 32-interval rows)
     ("per_row", dict(mode="bipolar", chunk_d=24, stoc_len=16), (90, 70, 5 * 24 + 10)),
     ("per_row", dict(mode="bipolar", chunk_d=26, stoc_len=16, rng_levels=16), (70, 90, 4 * 26)),
+    # odd chunks with 16- and 32-interval tables (widened to 64 intervals, one d per k-step)
+    ("per_row", dict(mode="bipolar", chunk_d=25, stoc_len=16), (80, 66, 4 * 25 + 7)),
+    ("per_row", dict(mode="bipolar", chunk_d=9, stoc_len=8, rng_levels=16), (40, 30, 5 * 9)),
+    ("per_row", dict(mode="bipolar", chunk_d=27, stoc_len=32), (70, 45, 3 * 27 + 11)),
     ("per_row", dict(mode="bipolar", halve_bipolar_stoc_len=True), (64, 64, 128)),
     ("per_tensor", dict(mode="bipolar"), (32, 64, 256)),
     ("per_tensor", dict(mode="unipolar"), (40, 33, 100)),

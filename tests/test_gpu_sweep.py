@@ -26,7 +26,7 @@ def _cases(seed, n):
         gran = str(rng.choice(["per_row", "per_row", "per_tensor"]))
         kw = dict(mode=mode, stoc_len=L, rng_levels=L)
         if gran == "per_row" and mode == "bipolar" and rng.random() < 0.3 and D > 40:
-            kw["chunk_d"] = int(rng.integers(8, D // 2)) // 2 * 2 or 8
+            kw["chunk_d"] = int(rng.integers(8, D // 2))        # odd or even
         if gran == "per_row" and mode == "unipolar" and rng.random() < 0.5:
             kw["group_a"], kw["group_b"] = int(rng.integers(1, 5)), int(rng.integers(1, 5))
         if gran == "per_tensor":

@@ -149,3 +149,21 @@ def test_classify_groups_by_range(capsys):
     assert classify_groups_by_range(w, 2, cfg, operator="fc2") == [16, 16, 64, 256]
     # one per-tensor group: its normalized range is 0, the lowest level
     assert classify_groups_by_range(w, 0, cfg) == [16]
+
+
+def test_mixed_row_check():
+    """sc_matmul_mixed's row validation (host logic on index tensors): bounds, repeats,
+    exact coverage."""
+    from scmp_kernels_amd.mp.dispatch import _check_rows
+    t = torch.tensor
+    assert _check_rows([t([0, 2, 4]), t([1, 3])], 5) is True
+    assert _check_rows([t([0, 2, 4]), t([1])], 5) is False
+    assert _check_rows([], 0) is True and _check_rows([], 3) is False
+    with pytest.raises(ValueError, match="more than once"):
+        _check_rows([t([0, 1, 2, 3]), t([3])], 5)      # duplicated 3 and missing 4
+    with pytest.raises(ValueError, match="more than once"):
+        _check_rows([t([0, 0])], 1)
+    with pytest.raises(ValueError, match=r"\[0, 5\)"):
+        _check_rows([t([0, 5])], 5)
+    with pytest.raises(ValueError, match=r"\[0, 5\)"):
+        _check_rows([t([-1, 2])], 5)
