@@ -203,8 +203,11 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         for (int i = 0; i < BA; ++i)
             c[i] = *(const uint2 *)(abase + (oa + 32u * (uint32_t)i * lda + 8u * (uint32_t)g));
         if (PERD) {
+            // an unconditional load (the index clamped to the last d; classes past D meet
+            // zero codes): a load under a branch makes the compiler wait for every load in
+            // flight, the code prefetches included, before the next one
             const int d = 8 * g + lane8;
-            cls = d < D ? P.d_class[d] : 0;
+            cls = P.d_class[d < D ? d : D - 1];
         }
         if (LUTSRC == LUT_RUNS) {
             // the group's class, by a vector load issued after the codes: waiting for it

@@ -44,6 +44,26 @@ def _check_rows(row_lists, N: int) -> bool:
     return seen == N
 
 
+def _checked_rows(assignment, originals, row_lists, N: int) -> bool:
+    """_check_rows with its host sync taken once per assignment: the result is kept on the
+    assignment together with the index tensors it checked, and holds for a later call
+    with the same N whose level tensors are the same objects at the same version (torch
+    bumps a tensor's version on every in-place change). Index tensors on the CPU are
+    checked there, with no device sync."""
+    if all(not t.is_cuda for t in originals):
+        return _check_rows([t.to(torch.int64) for t in originals], N)
+    key = (N, tuple((id(t), t._version) for t in originals))
+    seen = getattr(assignment, "_scmp_rows_checked", None)
+    if seen is not None and seen[0] == key and all(a is b for a, b in zip(seen[1], originals)):
+        return seen[2]
+    exact = _check_rows(row_lists, N)
+    try:
+        assignment._scmp_rows_checked = (key, list(originals), exact)
+    except AttributeError:
+        pass
+    return exact
+
+
 @torch.no_grad()
 def sc_matmul_mixed(a: torch.Tensor, b, assignment: RowAssignment, *, mode: str = "unipolar",
                     sc_prec: int = 8, group_a: int = 1, group_b: int = 1,
@@ -54,7 +74,10 @@ def sc_matmul_mixed(a: torch.Tensor, b, assignment: RowAssignment, *, mode: str 
     group_b=group_b, stoc_len=L, rng_levels=R, config=config, smooth_scales=...)`` with
     R = L (``rng_levels=None``, the mixed-precision convention) or the given rng_levels.
     The row groups of group_a follow each level's row order. ``b`` is an (M, D) weight or a
-    PreparedWeight of the same mode / sc_prec / group_b / smoothing."""
+    PreparedWeight of the same mode / sc_prec / group_b / smoothing. The row indices are
+    validated (in range, no row twice) once per assignment: the first call with device
+    index tensors syncs with the host, later calls with the same unmodified tensors do not.
+    Rows that no level names are zero."""
     if mode not in _VALID_MODES:
         raise ValueError(f"sc_matmul: unknown mode '{mode}'. Expected one of {_VALID_MODES}.")
     if not 1 <= sc_prec <= 8:
@@ -87,8 +110,10 @@ def sc_matmul_mixed(a: torch.Tensor, b, assignment: RowAssignment, *, mode: str 
         _check_smoothing_vector(smooth_scales, D, names=("a",))
         smooth = smooth_scales.to(device=dev, dtype=torch.float32).contiguous()
 
-    levels, pruned = [], []
+    levels, pruned, originals = [], [], []
     for L, rows in assignment.level_row_indices.items():
+        if rows.numel():
+            originals.append(rows)
         rows = rows.to(device=dev, dtype=torch.int64).contiguous()
         L = int(L)
         if rows.numel() == 0:
@@ -100,7 +125,7 @@ def sc_matmul_mixed(a: torch.Tensor, b, assignment: RowAssignment, *, mode: str 
             raise ValueError(f"sc_matmul: stoc_len={L} exceeds 2**sc_prec={2 ** sc_prec}; the "
                              f"RNG sequences are 2**sc_prec long.")
         levels.append((L, L if rng_levels is None else int(rng_levels), rows))
-    exact = _check_rows([r for _, _, r in levels] + pruned, N)
+    exact = _checked_rows(assignment, originals, [r for _, _, r in levels] + pruned, N)
     M = b.M if prepared else b.shape[0]
     with torch.cuda.device(dev):
         if prepared:

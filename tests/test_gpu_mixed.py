@@ -169,3 +169,34 @@ def test_mixed_rejects_repeated_rows_and_zero_fills_missing():
         ref = O.sc_matmul(a_h[r], b_h, "per_row", mode="bipolar", sc_prec=8, stoc_len=L,
                           rng_levels=L)
         np.testing.assert_array_equal(y.cpu().numpy()[r].view(np.uint32), ref.view(np.uint32))
+
+
+def test_mixed_row_check_syncs_once_per_assignment():
+    """The row validation's host sync runs on the first call with an assignment; a second
+    call with the same index tensors issues no synchronizing operation, and an in-place
+    change of an index tensor makes the next call check (and sync) again."""
+    from scmp_kernels_amd.mp import classify_rows_by_metric, sc_matmul_mixed
+    dev = _dev()
+    a_h, b_h, _ = _data(260, 130, 96, 8)
+    a, b = torch.from_numpy(a_h).to(dev), torch.from_numpy(b_h).to(dev)
+    ra = classify_rows_by_metric(a.abs().amax(dim=1), [256, 64], [0.5, 0.5])
+    y1 = sc_matmul_mixed(a, b, ra, mode="bipolar")
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        y2 = sc_matmul_mixed(a, b, ra, mode="bipolar")
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    np.testing.assert_array_equal(_bits(y2), _bits(y1))
+    rows = ra.level_row_indices[64]
+    rows.copy_(rows.flip(0))                     # same rows, new order: version bumped
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        with pytest.raises(RuntimeError):
+            sc_matmul_mixed(a, b, ra, mode="bipolar")
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    y3 = sc_matmul_mixed(a, b, ra, mode="bipolar")
+    ref = _loop(a, b, ra, mode="bipolar", sc_prec=8)
+    np.testing.assert_array_equal(_bits(y3), _bits(ref))
