@@ -184,7 +184,8 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream);
 #define SCMP_EPI_INT 0        /* iout[n, m] = I (int32) */
 #define SCMP_EPI_ROWCOL 1     /* fl(fl(I*c) * fl(sa[n]*sb[m])); per chunk, summed in order */
 #define SCMP_EPI_SCALAR 2     /* fl(fl(I*c) * s[0]) */
-#define SCMP_EPI_HEAD 3       /* fl(I * fl(c * s[batch])) */
+#define SCMP_EPI_HEAD 3       /* fl(I * fl(c * s[batch])); s NULL: s[batch] =
+                               * fl(sa[batch * sa_batch_stride] * sb[batch * sb_batch_stride]) */
 #define SCMP_EPI_ZP_ROWCOL 4  /* fl(fl(fl(I*c) + corr) * fl(sa*sb)), grouped zero-point */
 #define SCMP_EPI_ZP_SCALAR 5  /* fl(fl(fl(I*c) + corr) * s[0]), per-tensor zero-point */
 

@@ -61,7 +61,9 @@ struct EpiUniform {
 __device__ __forceinline__ EpiUniform epi_uniform(const scmp_epilogue &E, int64_t batch) {
     EpiUniform u = {0.f, 0.f, 0.f, 0.f};
     if (E.kind == SCMP_EPI_SCALAR) u.s = E.s[0];
-    else if (E.kind == SCMP_EPI_HEAD) u.s = E.s[batch];
+    else if (E.kind == SCMP_EPI_HEAD)   // s[batch], or the head's two scales' fp32 product
+        u.s = E.s ? E.s[batch]
+                  : __fmul_rn(E.sa[batch * E.sa_batch_stride], E.sb[batch * E.sb_batch_stride]);
     else if (E.kind == SCMP_EPI_ZP_SCALAR) {
         u.s = E.s[0];
         u.za = E.za[0];

@@ -34,8 +34,9 @@ __device__ __forceinline__ const float *x_row(const scmp_quant_args &a, int64_t 
     return a.x + (a.row_index ? a.row_index[r] : r) * a.ld;
 }
 
-__device__ __forceinline__ float load_x(const scmp_quant_args &a, int64_t r, int64_t c) {
-    float v = x_row(a, r)[c];
+// Element c of a row whose start (x_row) the caller has looked up once.
+__device__ __forceinline__ float load_x(const scmp_quant_args &a, const float *row, int64_t c) {
+    float v = row[c];
     if (a.smooth_mode == SCMP_SMOOTH_DIV) v = __fdiv_rn(v, a.smooth[c]);
     else if (a.smooth_mode == SCMP_SMOOTH_MUL) v = __fmul_rn(v, a.smooth[c]);
     return v;
@@ -85,8 +86,9 @@ __global__ void reduce_kernel(scmp_quant_args a, int64_t group, int64_t segw, in
         int64_t r = task / nseg, sgi = task - r * nseg;
         int64_t c0 = sgi * segw, c1 = c0 + segw < a.cols ? c0 + segw : a.cols;
         float mx = -INFINITY, mn = INFINITY, am = 0.0f;
+        const float *xr = x_row(a, r);
         for (int64_t c = c0 + lane; c < c1; c += 64) {
-            float v = load_x(a, r, c);
+            float v = load_x(a, xr, c);
             if (asym) {
                 mx = fmaxf(mx, v);
                 mn = fminf(mn, v);
@@ -258,10 +260,11 @@ __global__ void quantize_kernel(scmp_quant_args a, int64_t group, int64_t segw, 
         }
         const int64_t g = r / group;
         float rsum = 0.0f;
+        const float *xr = x_row(a, r);
         for (int64_t c = lane; c < a.cols; c += 64) {
             const int64_t sgi = c / segw;
             const QParams p = prm[g * nseg + sgi];
-            const float q = quant_value(a, p, load_x(a, r, c), qlo, qf);
+            const float q = quant_value(a, p, load_x(a, xr, c), qlo, qf);
             const uint8_t code = element_outputs(a, q, r, c, asym, rq, rf, qf);
             if (a.code) a.code[crow * a.code_ld + c] = code;
             rsum += q;                            // exact: integers below 2^24
@@ -299,6 +302,8 @@ constexpr int kGroupThreads = 256;
 constexpr int kGroupMaxRows = 1024;       // row sums of a group live in LDS
 constexpr int kMaxChunks = 16;            // register-held 4-column chunks per thread, max
 constexpr int kBigGroupThreads = 1024;    // threads of a workgroup for groups past 256 x 16
+constexpr int kBigChunks = 12;            // register-held chunks per thread at 1024 threads
+                                          // (128 registers: 16 would spill)
 
 enum { QOP_DIV = 0, QOP_DIVZP = 1, QOP_MUL = 2 };
 
@@ -327,35 +332,62 @@ struct __attribute__((aligned(4))) float4u {
     float x, y, z, w;
 };
 
-template <int SM>
-__device__ __forceinline__ void load_chunk4(const scmp_quant_args &a, int64_t r, int c,
-                                            bool vec, float (&v)[4]) {
-    const float *row = x_row(a, r);
-    if (c + 4 <= a.cols) {
-        float4 x4;
-        if (vec) {
-            x4 = *(const float4 *)(row + c);
-        } else {
-            const float4u u = *(const float4u *)(row + c);
-            x4 = make_float4(u.x, u.y, u.z, u.w);
-        }
-        v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;
-        if (SM != SCMP_SMOOTH_NONE) {
-            const float4u s4 = *(const float4u *)(a.smooth + c);
-            const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+// Chunk loads that never sit under a branch: a load inside a divergent branch (or one whose
+// address comes from an earlier load) makes the compiler wait for every load in flight at
+// the branch's end, which serializes a thread's chunks into one memory round trip each.
+// So a thread first issues the raw loads of all its chunks, with the chunk start clamped
+// into the row, and only then shifts, smooths and uses them.
+// MODE 0: rows 16-byte aligned and cols % 4 == 0 (one 16-byte load per chunk, no clamping);
+// MODE 1: cols >= 4, any row stride (four 4-byte loads at min(c, cols - 4));
+// MODE 2: cols < 4 (four loads at min(c + k, cols - 1)).
+template <int MODE>
+__device__ __forceinline__ void load_raw4(const float *row, int c, int cols, float (&t)[4]) {
+    if constexpr (MODE == 0) {
+        const float4 x4 = *(const float4 *)(row + c);
+        t[0] = x4.x; t[1] = x4.y; t[2] = x4.z; t[3] = x4.w;
+    } else if constexpr (MODE == 1) {
+        const int c0 = c < cols - 4 ? c : cols - 4;
+        const float4u u = *(const float4u *)(row + c0);
+        t[0] = u.x; t[1] = u.y; t[2] = u.z; t[3] = u.w;
+    } else {
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                v[k] = SM == SCMP_SMOOTH_DIV ? __fdiv_rn(v[k], sv[k]) : __fmul_rn(v[k], sv[k]);
-        }
-        return;
+        for (int k = 0; k < 4; ++k) t[k] = row[c + k < cols ? c + k : cols - 1];
     }
+}
+
+// Smoothing in the quantizer's fp32 order (x / s or x * s), then the chunk moved to start at
+// column c (MODE 1 loads a chunk that runs past the row end from cols - 4) and columns past
+// the row end set to 0.
+template <int MODE, int SM>
+__device__ __forceinline__ void finish4(int c, int cols, float (&t)[4], const float (&sv)[4]) {
+    if constexpr (SM != SCMP_SMOOTH_NONE) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        float x = c + k < a.cols ? row[c + k] : 0.0f;
-        if (SM == SCMP_SMOOTH_DIV && c + k < a.cols) x = __fdiv_rn(x, a.smooth[c + k]);
-        if (SM == SCMP_SMOOTH_MUL && c + k < a.cols) x = __fmul_rn(x, a.smooth[c + k]);
-        v[k] = x;
+        for (int k = 0; k < 4; ++k)
+            t[k] = SM == SCMP_SMOOTH_DIV ? __fdiv_rn(t[k], sv[k]) : __fmul_rn(t[k], sv[k]);
     }
+    if constexpr (MODE == 1) {
+        const int sh = c - (c < cols - 4 ? c : cols - 4);      // 0 except at a row end
+        if (sh != 0) {
+            float u[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) u[k] = t[k];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) t[k] = k + sh < 4 ? u[k + sh < 4 ? k + sh : 3] : 0.0f;
+        }
+    } else if constexpr (MODE == 2) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (c + k >= cols) t[k] = 0.0f;
+    }
+}
+
+// MODE of a quantizer call: 0 when every row start is 16-byte aligned and rows are whole
+// chunks, else 1 (2 for rows of fewer than 4 columns).
+__device__ __host__ __forceinline__ int chunk_mode(const scmp_quant_args &a) {
+    const bool aligned = (a.ld % 4 == 0) && (((uintptr_t)a.x & 15) == 0) &&
+                         (a.smooth == nullptr || ((uintptr_t)a.smooth & 15) == 0);
+    if (aligned && (a.cols & 3) == 0) return 0;
+    return a.cols >= 4 ? 1 : 2;
 }
 
 // Workgroup w of nw zeroes its share of the padding rows [cbr, code_rows) of every batch of
@@ -388,10 +420,12 @@ __device__ __forceinline__ void zero_pad_share(const scmp_quant_args &a, int64_t
 // PT: register-held chunks per thread (npt <= PT); npt > PT re-reads the chunks instead.
 template <int OP, int SM, int PT, int NT>
 __global__ void __launch_bounds__(NT)
-quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
+quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt) {
     __shared__ uint32_t red0[NT / 64], red1[NT / 64];
     __shared__ float rsums[kGroupMaxRows];
+    __shared__ int64_t s_rowoff[kGroupMaxRows];
     __shared__ uint8_t s_jtab[256];
+    constexpr bool SMOOTH = SM != SCMP_SMOOTH_NONE;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t r0 = (int64_t)blockIdx.x * G;
     const int nr = a.rows - r0 < G ? (int)(a.rows - r0) : G;
@@ -400,9 +434,26 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
     const bool want_sum = a.rowsum != nullptr;
     const bool thermo = a.code && a.code_kind == SCMP_CODE_THERMO;
     const bool lds_jtab = thermo && a.col_class == nullptr;
-    if (want_sum)
-        for (int i = tid; i < nr; i += NT) rsums[i] = 0.0f;
-    if (lds_jtab && tid < 256) s_jtab[tid] = a.jtab[tid];
+    // the thermometer table byte this thread places in LDS, loaded before any chunk (the
+    // oldest load: waiting for it waits for no chunk); written after the chunks' loads
+    const uint32_t jt = lds_jtab ? a.jtab[tid & 255] : 0u;
+    // the caller's row index, staged in LDS as element offsets (one read per row, so that no
+    // chunk load waits for its row's index); without one a row's start is computed
+    const bool ridx = a.row_index != nullptr;
+    if (ridx) {
+        for (int i = tid; i < nr; i += NT) s_rowoff[i] = a.row_index[r0 + i] * a.ld;
+        __syncthreads();
+    }
+    auto rowp = [&](int rr) __attribute__((always_inline)) {
+        return a.x + (ridx ? s_rowoff[rr] : (r0 + rr) * a.ld);
+    };
+    // chunk loads (load_raw4): one 16-byte load, or four clamped 4-byte ones; a uniform
+    // branch around a load whose value is used only after every load is issued
+    const bool m0 = chunk_mode(a) == 0;
+    auto load4 = [&](const float *row, int c, float (&t)[4]) __attribute__((always_inline)) {
+        if (m0) load_raw4<0>(row, c, a.cols, t);
+        else load_raw4<1>(row, c, a.cols, t);
+    };
 
     // position (row, first column) of this thread's k-th chunk, chunk index tid + 256 k;
     // a step of 256 chunks is dr rows and dc chunks
@@ -438,23 +489,58 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
             }
         }
     };
+    float sv[SMOOTH ? PT : 1][4];
+    // LDS tables written while the chunks' loads are in flight (read after the reduction's
+    // barrier)
+    auto write_tables = [&]() __attribute__((always_inline)) {
+        if (want_sum)
+            for (int i = tid; i < nr; i += NT) rsums[i] = 0.0f;
+        if (lds_jtab && tid < 256) s_jtab[tid] = (uint8_t)jt;
+    };
     if (reg) {
+        // every load first (a lane past the group's chunks loads chunk 0), then the values
         int rr = rr_first, cc = cc_first;
 #pragma unroll
         for (int k = 0; k < PT; ++k) {
+            const bool ok = k < npt && tid + k * NT < nch;
+            const int lc = ok ? 4 * cc : 0;
+            load4(rowp(ok ? rr : 0), lc, vals[k]);
+            if (SMOOTH) load4(a.smooth, lc, sv[SMOOTH ? k : 0]);
+            advance(rr, cc);
+        }
+        rr = rr_first;
+        cc = cc_first;
+        write_tables();
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
             if (k < npt && tid + k * NT < nch) {
-                load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, vals[k]);
+                finish4<1, SM>(4 * cc, a.cols, vals[k], sv[SMOOTH ? k : 0]);
                 fold(vals[k], 4 * cc);
             }
             advance(rr, cc);
         }
     } else {
+        write_tables();
+        // four chunks per step, loads first
         int rr = rr_first, cc = cc_first;
-        for (int ch = tid; ch < nch; ch += NT) {
-            float v[4];
-            load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, v);
-            fold(v, 4 * cc);
-            advance(rr, cc);
+        for (int ch = tid; ch < nch; ch += 4 * NT) {
+            float v[4][4], s4[SMOOTH ? 4 : 1][4];
+            int cu[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bool ok = ch + u * NT < nch;
+                cu[u] = 4 * cc;
+                load4(rowp(ok ? rr : 0), ok ? 4 * cc : 0, v[u]);
+                if (SMOOTH) load4(a.smooth, ok ? 4 * cc : 0, s4[SMOOTH ? u : 0]);
+                advance(rr, cc);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (ch + u * NT < nch) {
+                    finish4<1, SM>(cu[u], a.cols, v[u], s4[SMOOTH ? u : 0]);
+                    fold(v[u], cu[u]);
+                }
+            }
         }
     }
     uint32_t k0, k1 = 0;
@@ -610,11 +696,28 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
                 advance_code();
             }
         } else {
-            for (int ch = tid; ch < nch; ch += NT) {
-                float v[4];
-                load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, v);
-                emit_fast(v, rr, crow, 4 * cc);
-                advance_code();
+            for (int ch = tid; ch < nch; ch += 4 * NT) {
+                float v[4][4], s4[SMOOTH ? 4 : 1][4];
+                int ru[4], cu[4];
+                uint8_t *cru[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const bool ok = ch + u * NT < nch;
+                    ru[u] = rr;
+                    cu[u] = 4 * cc;
+                    cru[u] = crow;
+                    load4(rowp(ok ? rr : 0), ok ? 4 * cc : 0, v[u]);
+                    if (SMOOTH)
+                        load4(a.smooth, ok ? 4 * cc : 0, s4[SMOOTH ? u : 0]);
+                    advance_code();
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (ch + u * NT < nch) {
+                        finish4<1, SM>(cu[u], a.cols, v[u], s4[SMOOTH ? u : 0]);
+                        emit_fast(v[u], ru[u], cru[u], cu[u]);
+                    }
+                }
             }
         }
     } else if (reg) {
@@ -626,11 +729,25 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         }
     } else {
         int rr = rr_first, cc = cc_first;
-        for (int ch = tid; ch < nch; ch += NT) {
-            float v[4];
-            load_chunk4<SM>(a, r0 + rr, 4 * cc, vec, v);
-            emit(v, rr, 4 * cc);
-            advance(rr, cc);
+        for (int ch = tid; ch < nch; ch += 4 * NT) {
+            float v[4][4], s4[SMOOTH ? 4 : 1][4];
+            int ru[4], cu[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bool ok = ch + u * NT < nch;
+                ru[u] = rr;
+                cu[u] = 4 * cc;
+                load4(rowp(ok ? rr : 0), ok ? 4 * cc : 0, v[u]);
+                if (SMOOTH) load4(a.smooth, ok ? 4 * cc : 0, s4[SMOOTH ? u : 0]);
+                advance(rr, cc);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (ch + u * NT < nch) {
+                    finish4<1, SM>(cu[u], a.cols, v[u], s4[SMOOTH ? u : 0]);
+                    emit(v[u], ru[u], cu[u]);
+                }
+            }
         }
     }
     // zero code columns past the last 4-column chunk, per row of the group
@@ -652,6 +769,324 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt, bool vec) {
         if (a.zp) a.zp[r] = p.zp;
         if (want_sum) a.rowsum[r] = rsums[rr];
     }
+}
+
+// ---------------------------------------------------------------------------------
+// Lean one-pass group quantizer for the common case of the SC matmul: GEMM codes only (no
+// boundary / sign / integer outputs), thermometer codes from one table (jtab in LDS) or the
+// quantized integers as bytes, every chunk of the group held in registers. Same statistic,
+// parameters and per-element operations as quant_group_kernel, with the element path cut
+// to a few instructions: the code byte of q comes from one 512-entry LDS table indexed by
+// q (sign bit included), the clamp runs on the integer (equal for integer-valued rounded
+// quotients, NaN included: it converts to 0 either way), and the four code bytes of a chunk
+// are packed by shifts. CODE: SCMP_CODE_THERMO or SCMP_CODE_Q; SUM: row sums (zero-point
+// variant; the clamp then also runs in fp32, as the row sum adds the fp32 value). The load
+// mode and the smoothing are uniform branches around loads whose values are used only
+// after every load is issued.
+// ---------------------------------------------------------------------------------
+// DENSE: x rows, code rows and the group all contiguous (ld = code_ld = cols, a multiple of
+// 4, 16-byte aligned; no row index; no group across a batch): chunk k of a thread is chunk
+// tid + k * NT of the group in both buffers, so its addresses are fixed offsets.
+template <int OP, int PT, int NT, int CODE, bool SUM, bool SMOOTH, bool DENSE>
+__global__ void __launch_bounds__(NT)
+quant_codes_kernel(scmp_quant_args a, int G, int cpr, int npt) {
+    __shared__ uint32_t red0[NT / 64], red1[NT / 64];
+    __shared__ float rsums[SUM ? kGroupMaxRows : 1];
+    __shared__ int64_t s_rowoff[kGroupMaxRows];
+    __shared__ uint8_t s_code[CODE == SCMP_CODE_THERMO ? 512 : 1];
+    constexpr bool asym = OP == QOP_DIVZP;
+    const int sm = SMOOTH ? a.smooth_mode : SCMP_SMOOTH_NONE;
+    const bool m0 = chunk_mode(a) == 0;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * G;
+    const int nr = a.rows - r0 < G ? (int)(a.rows - r0) : G;
+    const int nch = nr * cpr;
+    const int qmax = a.q_max;
+    const int qlo = asym ? 0 : (a.variant == SCMP_Q_HEAD_SYM ? -(qmax + 1) : -qmax);
+    // the caller's row index, staged in LDS (one read per row); without one, a row's start
+    // is computed and the loads go out before any table is built
+    const bool ridx = a.row_index != nullptr;
+    if (ridx) {
+        for (int i = tid; i < nr; i += NT) s_rowoff[i] = a.row_index[r0 + i] * a.ld;
+        __syncthreads();
+    }
+    auto rowp = [&](int rr) __attribute__((always_inline)) {
+        return a.x + (ridx ? s_rowoff[rr] : (r0 + rr) * a.ld);
+    };
+
+    const int rr_first = tid / cpr;
+    const int cc_first = tid - rr_first * cpr;
+    const int dr = NT / cpr, dc = NT - dr * cpr;
+    auto advance = [&](int &rr, int &cc) __attribute__((always_inline)) {
+        cc += dc;
+        const bool wrap = cc >= cpr;
+        if (wrap) cc -= cpr;
+        rr += dr + (wrap ? 1 : 0);
+    };
+    // a chunk's element offset within the group's rows of x (ld apart) and of the codes
+    // (code_ld apart), tracked in 32 bits from the group's first row (groups hold fewer
+    // than 2^22 elements)
+    const uint32_t ld32 = (uint32_t)a.ld, cld32 = (uint32_t)a.code_ld;
+    const uint32_t xstep = (uint32_t)dr * ld32 + 4u * (uint32_t)dc, xwrap = ld32 - 4u * (uint32_t)cpr;
+    const uint32_t cstep = (uint32_t)dr * cld32 + 4u * (uint32_t)dc, cwrap = cld32 - 4u * (uint32_t)cpr;
+    auto advance_off = [&](int &rr, int &cc, uint32_t &xo, uint32_t &co)
+        __attribute__((always_inline)) {
+        cc += dc;
+        const bool wrap = cc >= cpr;
+        if (wrap) cc -= cpr;
+        rr += dr + (wrap ? 1 : 0);
+        xo += xstep + (wrap ? xwrap : 0u);
+        co += cstep + (wrap ? cwrap : 0u);
+    };
+    const float *xg = a.x + r0 * a.ld;                  // the group's first row (no row index)
+
+    // the thermometer table entries this thread will place in the code table, loaded first
+    // (the oldest load, so waiting for it waits for no chunk) with clamped indices
+    constexpr int NTAB = CODE == SCMP_CODE_THERMO ? (512 + NT - 1) / NT : 1;
+    uint32_t jt[NTAB];
+    if (CODE == SCMP_CODE_THERMO) {
+#pragma unroll
+        for (int j = 0; j < NTAB; ++j) {
+            const int q = (tid + j * NT) - 256;
+            const int m = q < 0 ? -q : q;
+            jt[j] = a.jtab[m < 255 ? m : 255];
+        }
+    }
+    // pass 1: every load, then the statistic
+    float vals[PT][4];
+    float sv[SMOOTH ? PT : 1][4];
+    {
+        int rr = rr_first, cc = cc_first;
+        uint32_t xo = (uint32_t)rr_first * ld32 + 4u * (uint32_t)cc_first, co = 0;
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            const bool ok = k < npt && tid + k * NT < nch;
+            const int lc = ok ? 4 * cc : 0;
+            if (DENSE) {
+                const float4 x4 = ((const float4 *)(a.x + r0 * a.cols))[ok ? tid + k * NT : 0];
+                vals[k][0] = x4.x; vals[k][1] = x4.y; vals[k][2] = x4.z; vals[k][3] = x4.w;
+                if (SMOOTH) load_raw4<0>(a.smooth, lc, a.cols, sv[SMOOTH ? k : 0]);
+            } else {
+                const float *row = ridx ? rowp(ok ? rr : 0) : xg + (ok ? xo - 4u * (uint32_t)cc : 0u);
+                if (m0) load_raw4<0>(row, lc, a.cols, vals[k]);
+                else load_raw4<1>(row, lc, a.cols, vals[k]);
+                if (SMOOTH) {
+                    if (m0) load_raw4<0>(a.smooth, lc, a.cols, sv[SMOOTH ? k : 0]);
+                    else load_raw4<1>(a.smooth, lc, a.cols, sv[SMOOTH ? k : 0]);
+                }
+            }
+            if (DENSE) {
+                if (SMOOTH || SUM) advance(rr, cc);
+            } else {
+                advance_off(rr, cc, xo, co);
+            }
+        }
+    }
+    // while the loads are in flight: row sums and the code table (read after the
+    // reduction's barrier)
+    if (SUM)
+        for (int i = tid; i < nr; i += NT) rsums[i] = 0.0f;
+    if (CODE == SCMP_CODE_THERMO) {
+        // code byte of q = i - 256 for the q the clamp lets through
+#pragma unroll
+        for (int j = 0; j < NTAB; ++j) {
+            const int i = tid + j * NT;
+            const int q = i - 256;
+            uint32_t c = (q >= qlo && q <= qmax) ? jt[j] : 0u;
+            if (!asym && q < 0) c |= 0x80u;
+            if (i < 512) s_code[i] = (uint8_t)c;
+        }
+    }
+    float mx = -INFINITY, mn = INFINITY, am = 0.0f;
+    const bool full = (a.cols & 3) == 0;
+    {
+        int rr = rr_first, cc = cc_first;
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            if (k < npt && tid + k * NT < nch) {
+                const int c = 4 * cc;
+                float (&svk)[4] = sv[SMOOTH ? k : 0];
+                if (SMOOTH && sm == SCMP_SMOOTH_DIV) finish4<1, SCMP_SMOOTH_DIV>(c, a.cols, vals[k], svk);
+                else if (SMOOTH && sm == SCMP_SMOOTH_MUL) finish4<1, SCMP_SMOOTH_MUL>(c, a.cols, vals[k], svk);
+                else if (!DENSE) finish4<1, SCMP_SMOOTH_NONE>(c, a.cols, vals[k], svk);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (asym && !DENSE && !full && c + e >= a.cols) break;
+                    if (asym) {
+                        mx = fmaxf(mx, vals[k][e]);
+                        mn = fminf(mn, vals[k][e]);
+                    } else {
+                        am = fmaxf(am, fabsf(vals[k][e]));
+                    }
+                }
+            }
+            if (!DENSE || SMOOTH || SUM) advance(rr, cc);
+        }
+    }
+    uint32_t k0, k1 = 0;
+    if (asym) {
+        mx = wave_max(mx);
+        mn = wave_min(mn);
+        k0 = key_of(mx);
+        k1 = key_of(-mn);
+    } else {
+        k0 = __float_as_uint(wave_max(am));
+    }
+    if (lane == 0) {
+        red0[wave] = k0;
+        red1[wave] = k1;
+    }
+    __syncthreads();
+    uint32_t s0 = red0[0], s1 = red1[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) {
+        s0 = s0 > red0[w] ? s0 : red0[w];
+        s1 = s1 > red1[w] ? s1 : red1[w];
+    }
+    const QParams p = derive_params(a, s0, asym ? s1 : 0u);
+
+    // pass 2: the code word of every chunk
+    const float qf = (float)qmax, qlof = (float)qlo;
+    const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+    const bool wave_rows = cpr % 64 == 0;
+    {
+        // DENSE: the group's first code row (r0's batch and row within it)
+        const int64_t gb = r0 / cbr;
+        uint32_t *cg = (uint32_t *)(a.code + (gb * a.code_rows + (r0 - gb * cbr)) * a.code_ld);
+        int rr = rr_first, cc = cc_first;
+        uint32_t xo = 0, co = (uint32_t)rr_first * cld32 + 4u * (uint32_t)cc_first;
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            if (k < npt && tid + k * NT < nch) {
+                const int c = 4 * cc;
+                const float (&v)[4] = vals[k];
+                float t[4];
+                if (OP == QOP_MUL) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) t[e] = rne(__fmul_rn(v[e], p.inv));
+                } else {
+                    bool ok = true;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float y = __fmul_rn(v[e], p.inv);
+                        const float u = OP == QOP_DIVZP ? __fadd_rn(y, p.zp) : y;
+                        t[e] = rne(u);
+                        ok = ok && __builtin_fabsf(y) < 1024.0f &&
+                             __builtin_fabsf(__fsub_rn(u, t[e])) < 0.5f - 4.8828125e-4f;
+                    }
+                    if (!ok) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float d = __fdiv_rn(v[e], p.s);
+                            t[e] = rne(OP == QOP_DIVZP ? __fadd_rn(d, p.zp) : d);
+                        }
+                    }
+                }
+                const int nv = DENSE ? 4 : a.cols - c;
+                uint32_t word = 0;
+                float qs = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    int qi = (int)t[e];
+                    qi = qi < qlo ? qlo : (qi > qmax ? qmax : qi);
+                    uint32_t code;
+                    if (CODE == SCMP_CODE_THERMO) code = s_code[qi + 256];
+                    else code = (uint32_t)(qi & 0xff);
+                    word |= (e < nv ? code : 0u) << (8 * e);
+                    if (SUM) qs += e < nv ? fmin_first(fmax_first(t[e], qlof), qf) : 0.0f;
+                }
+                if (DENSE) cg[tid + k * NT] = word;
+                else *(uint32_t *)((uint8_t *)cg + co) = word;
+                if (SUM) {
+                    if (wave_rows) {
+                        const float w = wave_sum(qs);
+                        if (lane == 0) atomicAdd(&rsums[rr], w);
+                    } else {
+                        atomicAdd(&rsums[rr], qs);
+                    }
+                }
+            }
+            // next chunk's row: the code row follows, skipping a batch's padding rows
+            if (DENSE) {
+                if (SUM) advance(rr, cc);
+            } else {
+                advance_off(rr, cc, xo, co);
+            }
+        }
+    }
+    // code columns past the last 4-column chunk, and the batches' padding rows
+    {
+        const int c0 = 4 * cpr;
+        const int tail = (int)(a.code_ld - c0);
+        for (int e = tid; e < nr * tail; e += NT) {
+            const int rr = e / tail, c = c0 + (e - rr * tail);
+            const int64_t r = r0 + rr, b = r / cbr, i = r - b * cbr;
+            a.code[(b * a.code_rows + i) * a.code_ld + c] = 0;
+        }
+    }
+    zero_pad_share<NT>(a, cbr, blockIdx.x, gridDim.x);
+    if (SUM) __syncthreads();
+    for (int rr = tid; rr < nr; rr += NT) {
+        const int64_t r = r0 + rr;
+        if (a.scale) a.scale[r] = p.s;
+        if (a.inv) a.inv[r] = p.inv;
+        if (a.zp) a.zp[r] = p.zp;
+        if (SUM) a.rowsum[r] = rsums[rr];
+    }
+}
+
+template <int OP, int PT, int NT>
+static void launch_codes(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt,
+                         hipStream_t stream) {
+    constexpr bool SUM = OP == QOP_DIVZP;
+    const bool th = a.code_kind == SCMP_CODE_THERMO;
+    const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+    const bool dense = chunk_mode(a) == 0 && a.ld == a.cols && a.code_ld == a.cols &&
+                       !a.row_index && cbr % G == 0;
+#define SCMP_LAUNCH_CODES(SMOOTH, DENSE)                                                      \
+    do {                                                                                     \
+        if (th)                                                                              \
+            quant_codes_kernel<OP, PT, NT, SCMP_CODE_THERMO, SUM, SMOOTH, DENSE>             \
+                <<<grid, NT, 0, stream>>>(a, G, cpr, npt);                                   \
+        else                                                                                 \
+            quant_codes_kernel<OP, PT, NT, SCMP_CODE_Q, SUM, SMOOTH, DENSE>                  \
+                <<<grid, NT, 0, stream>>>(a, G, cpr, npt);                                   \
+    } while (0)
+    if (a.smooth_mode != SCMP_SMOOTH_NONE) {
+        if (dense) SCMP_LAUNCH_CODES(true, true);
+        else SCMP_LAUNCH_CODES(true, false);
+    } else {
+        if (dense) SCMP_LAUNCH_CODES(false, true);
+        else SCMP_LAUNCH_CODES(false, false);
+    }
+#undef SCMP_LAUNCH_CODES
+}
+
+// The lean kernel's launch for a call it covers (codes only, one thermometer table or byte
+// codes, row sums exactly for the zero-point variant, every chunk in registers); false:
+// not covered.
+template <int OP>
+static bool try_codes(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt, bool wide,
+                      hipStream_t stream) {
+    if (!a.code || a.beta16 || a.beta32 || a.sign || a.xint || a.cols < 4) return false;
+    if (a.code_kind == SCMP_CODE_THERMO && a.col_class != nullptr) return false;
+    if ((a.rowsum != nullptr) != (OP == QOP_DIVZP)) return false;
+    const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+    if (cbr % G != 0 && cbr < a.rows) return false;      // a group across a batch boundary
+    if (wide) {
+        launch_codes<OP, 4, kBigGroupThreads>(a, grid, G, cpr,
+                                              (int)cdiv((int64_t)G * cpr, kBigGroupThreads), stream);
+    } else if (npt <= 4) {
+        launch_codes<OP, 4, kGroupThreads>(a, grid, G, cpr, npt, stream);
+    } else if (npt <= kMaxChunks) {
+        launch_codes<OP, kMaxChunks, kGroupThreads>(a, grid, G, cpr, npt, stream);
+    } else if (OP == QOP_MUL && cdiv((int64_t)G * cpr, kBigGroupThreads) <= kBigChunks) {
+        launch_codes<QOP_MUL, kBigChunks, kBigGroupThreads>(
+            a, grid, G, cpr, (int)cdiv((int64_t)G * cpr, kBigGroupThreads), stream);
+    } else {
+        return false;
+    }
+    return true;
 }
 
 // Zero the padding rows [code_batch_rows, code_rows) of every batch of a code buffer.
@@ -691,7 +1126,7 @@ constexpr int kMaxSegs = 256;
 
 template <int OP, int SM, int PT>
 __global__ void __launch_bounds__(kGroupThreads)
-quant_seg_kernel(scmp_quant_args a, int cpr, int segw, int nseg, bool vec) {
+quant_seg_kernel(scmp_quant_args a, int cpr, int segw, int nseg) {
     __shared__ uint32_t s_st0[kMaxSegs], s_st1[kMaxSegs];
     __shared__ QParams s_prm[kMaxSegs];
     __shared__ uint8_t s_jtab[256];
@@ -701,18 +1136,37 @@ quant_seg_kernel(scmp_quant_args a, int cpr, int segw, int nseg, bool vec) {
     constexpr bool asym = OP == QOP_DIVZP;
     const bool thermo = a.code && a.code_kind == SCMP_CODE_THERMO;
     const bool lds_jtab = thermo && a.col_class == nullptr;
+    // the thermometer table byte of this thread, loaded before any chunk (see below)
+    const uint32_t jt = lds_jtab ? a.jtab[tid] : 0u;
+
+    constexpr bool SMOOTH = SM != SCMP_SMOOTH_NONE;
+    const float *xr = x_row(a, r);
+    const bool m0 = chunk_mode(a) == 0;
+    float vals[PT][4];
+    float sv[SMOOTH ? PT : 1][4];
+    // every load first (a lane past the row's chunks loads chunk 0), then the values
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+        const int cc = tid + k * kGroupThreads;
+        const int lc = cc < cpr ? 4 * cc : 0;
+        if (m0) load_raw4<0>(xr, lc, a.cols, vals[k]);
+        else load_raw4<1>(xr, lc, a.cols, vals[k]);
+        if (SMOOTH) {
+            if (m0) load_raw4<0>(a.smooth, lc, a.cols, sv[SMOOTH ? k : 0]);
+            else load_raw4<1>(a.smooth, lc, a.cols, sv[SMOOTH ? k : 0]);
+        }
+    }
+    // LDS state, set up while the loads are in flight
     for (int t = tid; t < nseg; t += kGroupThreads) s_st0[t] = s_st1[t] = 0u;
-    if (lds_jtab) s_jtab[tid] = a.jtab[tid];
+    if (lds_jtab) s_jtab[tid] = (uint8_t)jt;
     if (tid == 0) s_rsum = 0.0f;
     __syncthreads();
-
-    float vals[PT][4];
 #pragma unroll
     for (int k = 0; k < PT; ++k) {
         const int cc = tid + k * kGroupThreads;
         if (cc < cpr) {
             const int c = 4 * cc;
-            load_chunk4<SM>(a, r, c, vec, vals[k]);
+            finish4<1, SM>(c, a.cols, vals[k], sv[SMOOTH ? k : 0]);
             float mx = -INFINITY, mn = INFINITY, am = 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -794,21 +1248,21 @@ quant_seg_kernel(scmp_quant_args a, int cpr, int segw, int nseg, bool vec) {
 }
 
 template <int OP, int PT>
-static void launch_seg_pt(const scmp_quant_args &a, int cpr, int segw, int nseg, bool vec,
+static void launch_seg_pt(const scmp_quant_args &a, int cpr, int segw, int nseg,
                           hipStream_t stream) {
     const dim3 grid((unsigned)a.rows);
     switch (a.smooth_mode) {
     case SCMP_SMOOTH_DIV:
         quant_seg_kernel<OP, SCMP_SMOOTH_DIV, PT><<<grid, kGroupThreads, 0, stream>>>(
-            a, cpr, segw, nseg, vec);
+            a, cpr, segw, nseg);
         break;
     case SCMP_SMOOTH_MUL:
         quant_seg_kernel<OP, SCMP_SMOOTH_MUL, PT><<<grid, kGroupThreads, 0, stream>>>(
-            a, cpr, segw, nseg, vec);
+            a, cpr, segw, nseg);
         break;
     default:
         quant_seg_kernel<OP, SCMP_SMOOTH_NONE, PT><<<grid, kGroupThreads, 0, stream>>>(
-            a, cpr, segw, nseg, vec);
+            a, cpr, segw, nseg);
         break;
     }
 }
@@ -817,21 +1271,19 @@ static void launch_seg_pt(const scmp_quant_args &a, int cpr, int segw, int nseg,
 static int quantize_segments(const scmp_quant_args &a, int64_t segw, int64_t nseg,
                              hipStream_t stream) {
     const int cpr = (int)cdiv(a.cols, 4);
-    const bool vec = (a.ld % 4 == 0) && (((uintptr_t)a.x & 15) == 0) &&
-                     (a.smooth_mode == SCMP_SMOOTH_NONE || ((uintptr_t)a.smooth & 15) == 0);
     const bool small = cpr <= 4 * kGroupThreads;
     switch (a.variant) {
     case SCMP_Q_GROUP_SYM:
-        if (small) launch_seg_pt<QOP_DIV, 4>(a, cpr, (int)segw, (int)nseg, vec, stream);
-        else launch_seg_pt<QOP_DIV, kMaxChunks>(a, cpr, (int)segw, (int)nseg, vec, stream);
+        if (small) launch_seg_pt<QOP_DIV, 4>(a, cpr, (int)segw, (int)nseg, stream);
+        else launch_seg_pt<QOP_DIV, kMaxChunks>(a, cpr, (int)segw, (int)nseg, stream);
         break;
     case SCMP_Q_GROUP_ASYM:
-        if (small) launch_seg_pt<QOP_DIVZP, 4>(a, cpr, (int)segw, (int)nseg, vec, stream);
-        else launch_seg_pt<QOP_DIVZP, kMaxChunks>(a, cpr, (int)segw, (int)nseg, vec, stream);
+        if (small) launch_seg_pt<QOP_DIVZP, 4>(a, cpr, (int)segw, (int)nseg, stream);
+        else launch_seg_pt<QOP_DIVZP, kMaxChunks>(a, cpr, (int)segw, (int)nseg, stream);
         break;
     default:
-        if (small) launch_seg_pt<QOP_MUL, 4>(a, cpr, (int)segw, (int)nseg, vec, stream);
-        else launch_seg_pt<QOP_MUL, kMaxChunks>(a, cpr, (int)segw, (int)nseg, vec, stream);
+        if (small) launch_seg_pt<QOP_MUL, 4>(a, cpr, (int)segw, (int)nseg, stream);
+        else launch_seg_pt<QOP_MUL, kMaxChunks>(a, cpr, (int)segw, (int)nseg, stream);
         break;
     }
     SCMP_LAUNCH_CHECK("scmp_quantize/segments");
@@ -853,19 +1305,16 @@ static int quantize_segments(const scmp_quant_args &a, int64_t segw, int64_t nse
 // smoothing mode and the register-held chunk count (4: rows up to 4096 columns; 16).
 template <int OP, int PT, int NT = kGroupThreads>
 static void launch_group_pt(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt,
-                            bool vec, hipStream_t stream) {
+                            hipStream_t stream) {
     switch (a.smooth_mode) {
     case SCMP_SMOOTH_DIV:
-        quant_group_kernel<OP, SCMP_SMOOTH_DIV, PT, NT><<<grid, NT, 0, stream>>>(
-            a, G, cpr, npt, vec);
+        quant_group_kernel<OP, SCMP_SMOOTH_DIV, PT, NT><<<grid, NT, 0, stream>>>(a, G, cpr, npt);
         break;
     case SCMP_SMOOTH_MUL:
-        quant_group_kernel<OP, SCMP_SMOOTH_MUL, PT, NT><<<grid, NT, 0, stream>>>(
-            a, G, cpr, npt, vec);
+        quant_group_kernel<OP, SCMP_SMOOTH_MUL, PT, NT><<<grid, NT, 0, stream>>>(a, G, cpr, npt);
         break;
     default:
-        quant_group_kernel<OP, SCMP_SMOOTH_NONE, PT, NT><<<grid, NT, 0, stream>>>(
-            a, G, cpr, npt, vec);
+        quant_group_kernel<OP, SCMP_SMOOTH_NONE, PT, NT><<<grid, NT, 0, stream>>>(a, G, cpr, npt);
         break;
     }
 }
@@ -876,20 +1325,19 @@ static void launch_group_pt(const scmp_quant_args &a, dim3 grid, int G, int cpr,
 // also take 1024 threads, four times the loads in flight per group.
 template <int OP>
 static void launch_group(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt,
-                         bool vec, bool wide, hipStream_t stream) {
+                         bool wide, hipStream_t stream) {
     if (wide) {
         launch_group_pt<OP, 4, kBigGroupThreads>(a, grid, G, cpr,
                                                  (int)cdiv((int64_t)G * cpr, kBigGroupThreads),
-                                                 vec, stream);
+                                                 stream);
     } else if (npt <= 4) {
-        launch_group_pt<OP, 4>(a, grid, G, cpr, npt, vec, stream);
+        launch_group_pt<OP, 4>(a, grid, G, cpr, npt, stream);
     } else if (npt <= kMaxChunks || OP != QOP_MUL) {
-        launch_group_pt<OP, kMaxChunks>(a, grid, G, cpr, npt, vec, stream);
+        launch_group_pt<OP, kMaxChunks>(a, grid, G, cpr, npt, stream);
     } else {
         const int64_t per = cdiv((int64_t)G * cpr, kBigGroupThreads);
-        const int npt4 = (int)(per <= kMaxChunks ? per : kMaxChunks + 1);
-        launch_group_pt<QOP_MUL, kMaxChunks, kBigGroupThreads>(a, grid, G, cpr, npt4, vec,
-                                                               stream);
+        const int npt4 = (int)(per <= kBigChunks ? per : kBigChunks + 1);
+        launch_group_pt<QOP_MUL, kBigChunks, kBigGroupThreads>(a, grid, G, cpr, npt4, stream);
     }
 }
 
@@ -916,22 +1364,23 @@ static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stre
     const bool wide = ngroups < 2 * (int64_t)quant_cu_count() && G * cpr > kBigGroupThreads &&
                       G * cpr <= 4 * (int64_t)kBigGroupThreads;
     const int64_t per = cdiv(G * cpr, kGroupThreads);
-    const bool vec = (a.ld % 4 == 0) && (((uintptr_t)a.x & 15) == 0) &&
-                     (a.smooth_mode == SCMP_SMOOTH_NONE || ((uintptr_t)a.smooth & 15) == 0);
     const dim3 grid((unsigned)ngroups);
     const int npt = (int)(per <= kMaxChunks ? per : kMaxChunks + 1);   // at 256 threads
     switch (a.variant) {
     case SCMP_Q_GROUP_SYM:
-        launch_group<QOP_DIV>(a, grid, (int)G, (int)cpr, npt, vec, wide, stream);
+        if (!try_codes<QOP_DIV>(a, grid, (int)G, (int)cpr, npt, wide, stream))
+            launch_group<QOP_DIV>(a, grid, (int)G, (int)cpr, npt, wide, stream);
         break;
     case SCMP_Q_GROUP_ASYM:
-        launch_group<QOP_DIVZP>(a, grid, (int)G, (int)cpr, npt, vec, wide, stream);
+        if (!try_codes<QOP_DIVZP>(a, grid, (int)G, (int)cpr, npt, wide, stream))
+            launch_group<QOP_DIVZP>(a, grid, (int)G, (int)cpr, npt, wide, stream);
         break;
     default:
-        launch_group<QOP_MUL>(a, grid, (int)G, (int)cpr, npt, vec, wide, stream);
+        if (!try_codes<QOP_MUL>(a, grid, (int)G, (int)cpr, npt, wide, stream))
+            launch_group<QOP_MUL>(a, grid, (int)G, (int)cpr, npt, wide, stream);
         break;
     }
-    SCMP_LAUNCH_CHECK("scmp_quantize/group");   // the kernel zeroes the padding rows too
+    SCMP_LAUNCH_CHECK("scmp_quantize/group");   // the kernels zero the padding rows too
     return SCMP_OK;
 }
 
@@ -1004,7 +1453,7 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
         SCMP_LAUNCH_CHECK("scmp_quantize/given");
     }
     if (!given && !host && !tensor && nseg == 1 && G <= kGroupMaxRows && G * a.cols <= (1 << 22) &&
-        (!a.code || a.code_ld % 4 == 0))
+        a.cols >= 4 && (!a.code || a.code_ld % 4 == 0))
         return quantize_groups(a, G, stream);
     if (!given && !host && !tensor && nseg > 1 && G == 1 && nseg <= kMaxSegs && segw % 4 == 0 &&
         a.cols <= 4 * kGroupThreads * kMaxChunks && (!a.code || a.code_ld % 4 == 0))

@@ -709,12 +709,13 @@ def _sc_matmul_per_head_bipolar(q_flat, k_flat, q_maxs=None, q_mins=None, k_maxs
     w2 = quantize(k_flat.reshape(BH * M, D), _lib.Q_HEAD_SYM, Q, R, group=M, smooth=s_b,
                   smooth_mode=m_b, code=cb, code_kind=_lib.CODE_Q, code_batch_rows=M, scale=sk,
                   given_absmax=gk)
-    # out_scale = scale_q * scale_k (kernels.py:550), fp32
-    hs = (sq[::N] * sk[::M]).contiguous()
+    # out_scale = scale_q * scale_k (kernels.py:550), fp32: the kernel multiplies the
+    # head's first row scales (every row of a head has the head's scale)
     y = torch.empty((BH, N, M), dtype=torch.float32, device=dev)
     epi = _lib.Epilogue()
     epi.kind, epi.c = _lib.EPI_HEAD, _inner_scale(Q, stoc_len)
-    epi.s = hs.data_ptr()
+    epi.sa, epi.sb = sq.data_ptr(), sk.data_ptr()
+    epi.sa_batch_stride, epi.sb_batch_stride = N, M
     sc_gemm(ca, cb, N=N, M=M, D=D, batch=BH, tabs=tabs, epi=epi, y=y, bsy=N * M)
     del w1, w2
     return y.to(home) if home is not None else y
