@@ -58,8 +58,8 @@ enum { LUT_LDS = 0, LUT_LDS_CLASSES = 1, LUT_GLOBAL = 2, LUT_RUNS = 3 };
 
 // floats of the per-tile epilogue area: 3 factors per row and per column, then one int64
 // output offset per row (two floats' worth each), for the largest tile shapes: 256 x 256
-// (2048 floats) and 128 x 512 (2176)
-constexpr int kFactorFloats = 5 * 128 + 3 * 512;
+// (2048 floats) and 128 x 512 (2176), then the finisher flag (one int, padded to 16 bytes)
+constexpr int kFactorFloats = 5 * 128 + 3 * 512 + 4;
 
 // Tile shapes of the persistent kernel (rows of A x rows of B per workgroup, four waves):
 // 256 x 256 (2 x 2 waves of 128 x 128), narrow 256 x 64 (4 x 1 waves of 64 x 64) for outputs
@@ -104,13 +104,16 @@ __device__ __forceinline__ void interleave_unit() {
     }
 }
 
-// LDS layout of both kernels: [thermometer table | stream table(s) | epilogue factors].
+// LDS layout of both kernels: the thermometer table is a static array (its address is a
+// compile-time constant, so a lookup's address is its scaled code with the base in the
+// read's offset field), then the dynamic area [stream table(s) | epilogue factors].
+// Bytes of the stream tables in the dynamic area:
 template <int JPF, int LUTSRC>
 __device__ __forceinline__ int fp4_tables_bytes(const GemmP &P) {
     using G = Fp4Geom<JPF>;
-    return G::TAB * (1 + (LUTSRC == LUT_LDS || LUTSRC == LUT_RUNS ? 1
-                          : LUTSRC == LUT_LDS_CLASSES                ? P.nclass
-                                                                     : 0));
+    return G::TAB * (LUTSRC == LUT_LDS || LUTSRC == LUT_RUNS ? 1
+                     : LUTSRC == LUT_LDS_CLASSES                ? P.nclass
+                                                                : 0);
 }
 
 // Copies `rows` stored table rows (ROWB bytes apart) into LDS rows LS bytes apart.
@@ -191,14 +194,17 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     const int glast = ngroups >= 2 ? ngroups - 2 : 0;   // last pair address (in groups)
 
     // With per-d table classes, lane l also loads the class of inner dimension 8g + (l & 7)
-    // of each group into cls; a unit takes its d's class from that lane (v_readlane), so the
-    // class costs no memory wait inside the loop.
+    // of each group into cls.x; a unit takes its d's class from that lane (v_readlane), so
+    // the class costs no memory wait inside the loop. JPF = 16: each lane loads the classes
+    // of the four inner dimensions its lane half takes in the group's two units (cls.x, .y:
+    // d = 8g + 2h, +1; cls.z, .w: d = 8g + 4 + 2h, +1), so a unit's table bases need no
+    // cross-lane moves.
     const int lane8 = (int)(threadIdx.x & 7);
     // lane offsets of row li of block 0 (a block is 32 rows further); all below 2^31, as
     // the host bounds D (and so the row strides) by 65536
     const uint32_t lda = (uint32_t)P.lda, ldb = (uint32_t)P.ldb;
     const uint32_t oa = (uint32_t)li * lda, ob = (uint32_t)li * ldb;
-    auto load_a = [&](uint2 (&c)[BA], int &cls, int g) __attribute__((always_inline)) {
+    auto load_a = [&](uint2 (&c)[BA], int4 &cls, int g) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < BA; ++i)
             c[i] = *(const uint2 *)(abase + (oa + 32u * (uint32_t)i * lda + 8u * (uint32_t)g));
@@ -206,15 +212,25 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             // an unconditional load (the index clamped to the last d; classes past D meet
             // zero codes): a load under a branch makes the compiler wait for every load in
             // flight, the code prefetches included, before the next one
-            const int d = 8 * g + lane8;
-            cls = P.d_class[d < D ? d : D - 1];
+            if constexpr (JPF == 16) {
+                // 32-bit indices: scalar base + vector offset addressing
+                const uint32_t dmax = (uint32_t)D - 1u;
+                const uint32_t d0 = 8u * (uint32_t)g + 2u * (uint32_t)h;
+                cls.x = P.d_class[d0 < dmax ? d0 : dmax];
+                cls.y = P.d_class[d0 + 1u < dmax ? d0 + 1u : dmax];
+                cls.z = P.d_class[d0 + 4u < dmax ? d0 + 4u : dmax];
+                cls.w = P.d_class[d0 + 5u < dmax ? d0 + 5u : dmax];
+            } else {
+                const int d = 8 * g + lane8;
+                cls.x = P.d_class[d < D ? d : D - 1];
+            }
         }
         if (LUTSRC == LUT_RUNS) {
             // the group's class, by a vector load issued after the codes: waiting for it
             // waits for nothing that is not needed at the same point
             int z = 0;
             asm volatile("" : "+v"(z));
-            cls = P.group_class[g + z];
+            cls.x = P.group_class[g + z];
         }
     };
     // a pair starts at an odd group as often as at an even one: 8-byte aligned 16-byte loads
@@ -243,10 +259,13 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         return (int)((w >> (8 * (dl & 3))) & 0xffu);
     };
     // JPF <= 32: the lane half h selects which code bytes of a word it takes. Rotating the
-    // word right by `rot` bits (8h or 16h) moves them to fixed byte positions, so a lookup
-    // costs a constant-position byte extract instead of a variable shift; word w of row i
-    // (w = 0, 1: the group's d 0-3, 4-7), byte t after the rotation.
-    const uint32_t rot = (JPF == 16 ? 16u : 8u) * (uint32_t)h;
+    // word right by `rot` bits moves them to fixed byte positions, so a lookup costs a
+    // constant-position byte extract instead of a variable shift; word w of row i (w = 0, 1:
+    // the group's d 0-3, 4-7), byte t after the rotation. JPF = 16 rotates by 24 - 16h, which
+    // puts the half's bytes 2h, 2h + 1 at positions 1 and 2: a byte there is extracted and
+    // scaled to a row offset by one instruction (a shift with a byte-select operand); JPF = 32
+    // rotates by 8h.
+    const uint32_t rot = JPF == 16 ? 24u - 16u * (uint32_t)h : 8u * (uint32_t)h;
     auto rbyte = [&](uint32_t w, int t) __attribute__((always_inline)) {
         return (int)((__builtin_amdgcn_alignbit(w, w, rot) >> (8 * t)) & 0xffu);
     };
@@ -260,39 +279,35 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
 
     // JPF = 16: the lane half's two inner dimensions dl, dl + 1 of a unit, 8 bytes (16
     // intervals) of a table row each, side by side in one fragment
-    auto stage16 = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&ca)[BA], int cls8,
+    auto stage16 = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&ca)[BA], int4 cls4,
                        const uint4 (&qb)[BB], int m, int unit) __attribute__((always_inline)) {
-        // d 4 unit + 2h and + 1: bytes 0 and 1 of word `unit` rotated by 16h
+        // d 4 unit + 2h and + 1: bytes 1 and 2 of word `unit` rotated by 24 - 16h
 #pragma unroll
         for (int i = 0; i < BA; ++i) {
-            const uint2 r0 = *(const uint2 *)(sA + rcode_a(ca, i, unit, 0) * LS);
-            const uint2 r1 = *(const uint2 *)(sA + rcode_a(ca, i, unit, 1) * LS);
+            const uint2 r0 = *(const uint2 *)(sA + rcode_a(ca, i, unit, 1) * LS);
+            const uint2 r1 = *(const uint2 *)(sA + rcode_a(ca, i, unit, 2) * LS);
             F.a[i][0] = (v4i){(int)r0.x, (int)r0.y, (int)r1.x, (int)r1.y};
         }
         const uint8_t *base0 = sB, *base1 = sB;
         if (PERD) {
-            const int c0 = __builtin_amdgcn_readlane(cls8, 4 * unit);
-            const int c1 = __builtin_amdgcn_readlane(cls8, 4 * unit + 1);
-            const int c2 = __builtin_amdgcn_readlane(cls8, 4 * unit + 2);
-            const int c3 = __builtin_amdgcn_readlane(cls8, 4 * unit + 3);
-            const int k0 = h ? c2 : c0, k1 = h ? c3 : c1;
+            const int k0 = unit ? cls4.z : cls4.x, k1 = unit ? cls4.w : cls4.y;
             base0 = LUTSRC == LUT_GLOBAL ? glut + (int64_t)k0 * 256 * ROWB : sB + k0 * TAB;
             base1 = LUTSRC == LUT_GLOBAL ? glut + (int64_t)k1 * 256 * ROWB : sB + k1 * TAB;
         }
         constexpr int RS = LUTSRC == LUT_GLOBAL ? ROWB : LS;
 #pragma unroll
         for (int j = 0; j < BB; ++j) {
-            const uint2 r0 = *(const uint2 *)(base0 + rcode_b(qb, m, j, unit, 0) * RS);
-            const uint2 r1 = *(const uint2 *)(base1 + rcode_b(qb, m, j, unit, 1) * RS);
+            const uint2 r0 = *(const uint2 *)(base0 + rcode_b(qb, m, j, unit, 1) * RS);
+            const uint2 r1 = *(const uint2 *)(base1 + rcode_b(qb, m, j, unit, 2) * RS);
             F.b[j][0] = (v4i){(int)r0.x, (int)r0.y, (int)r1.x, (int)r1.y};
         }
     };
     // load unit `unit` of the group whose first d is dg (A codes ca, B codes: half m of qb)
-    auto stage = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&ca)[BA], int cls8,
+    auto stage = [&](Fp4Frag<JPF, BA, BB> &F, const uint2 (&ca)[BA], int4 cls4,
                      const uint4 (&qb)[BB], int m, int unit, int dg)
         __attribute__((always_inline)) {
         if constexpr (JPF == 16) {
-            stage16(F, ca, cls8, qb, m, unit);
+            stage16(F, ca, cls4, qb, m, unit);
             return;
         }
         const int dl = JPF == 32 ? 2 * unit + h : unit / SPD;    // d within the group
@@ -310,11 +325,11 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
         if (PERD) {
             int cls;
             if (JPF == 32) {                     // the lane halves take d = 2 unit + h
-                const int c0 = __builtin_amdgcn_readlane(cls8, 2 * unit);
-                const int c1 = __builtin_amdgcn_readlane(cls8, 2 * unit + 1);
+                const int c0 = __builtin_amdgcn_readlane(cls4.x, 2 * unit);
+                const int c1 = __builtin_amdgcn_readlane(cls4.x, 2 * unit + 1);
                 cls = h ? c1 : c0;
             } else {
-                cls = __builtin_amdgcn_readlane(cls8, unit / SPD);
+                cls = __builtin_amdgcn_readlane(cls4.x, unit / SPD);
             }
             base = LUTSRC == LUT_GLOBAL ? glut + (int64_t)cls * 256 * ROWB : sB + cls * TAB;
         }
@@ -354,8 +369,8 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     Fp4Frag<JPF, BA, BB> F0, F1;
     // one group g (A codes ca, B codes half m of qb); its last unit stages unit 0 of the
     // next group (A codes can, B codes half mn of qbn), then runs `refill`
-    auto group = [&](const uint2 (&ca)[BA], int cls, const uint4 (&qb)[BB], int m, int g,
-                     const uint2 (&can)[BA], int clsn, const uint4 (&qbn)[BB], int mn,
+    auto group = [&](const uint2 (&ca)[BA], int4 cls, const uint4 (&qb)[BB], int m, int g,
+                     const uint2 (&can)[BA], int4 clsn, const uint4 (&qbn)[BB], int mn,
                      auto refill) __attribute__((always_inline)) {
         const int dg = 8 * g;
 #pragma unroll
@@ -371,8 +386,8 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
                 stage(F0, ca, cls, qb, m, uu + 2, dg);
             } else {
                 if (LUTSRC == LUT_RUNS) {
-                    const int cn = __builtin_amdgcn_readfirstlane(clsn);
-                    if (cn != __builtin_amdgcn_readfirstlane(cls)) run_table(cn);
+                    const int cn = __builtin_amdgcn_readfirstlane(clsn.x);
+                    if (cn != __builtin_amdgcn_readfirstlane(cls.x)) run_table(cn);
                 }
                 stage(F0, can, clsn, qbn, mn, 0, dg + 8);
                 refill();
@@ -390,13 +405,13 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     // qn the pair (g+2, g+3), in flight
     uint2 a0[BA], a1[BA];
     uint4 qc[BB], qn[BB];
-    int cl0 = 0, cl1 = 0;
+    int4 cl0 = {0, 0, 0, 0}, cl1 = {0, 0, 0, 0};
     load_a(a0, cl0, g0);
     load_a(a1, cl1, g0 + 1 < g1 ? g0 + 1 : g1 - 1);
     load_b(qc, g0);
     load_b(qn, g0 + 2);
     int sc = shift_of(g0);                       // 1 only for a lone last group
-    if (LUTSRC == LUT_RUNS) run_table(__builtin_amdgcn_readfirstlane(cl0));
+    if (LUTSRC == LUT_RUNS) run_table(__builtin_amdgcn_readfirstlane(cl0.x));
     stage(F0, a0, cl0, qc, sc, 0, 8 * g0);
     int g = g0;
     // full pairs: g + 1 < g1 <= ngroups, so qc's shift is 0; the loop body has no branch
@@ -492,15 +507,17 @@ sc_gemm_fp4_kernel(GemmP P) {
     constexpr int NW = WA * WB;
     constexpr int TILE_FLOATS = NW * BA * BB * 1024;   // accumulators of one tile
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int s_last;
+    __shared__ __attribute__((aligned(16))) uint8_t sA[Fp4Geom<JPF>::TAB];  // thermometer
     const int tabs = fp4_tables_bytes<JPF, LUTSRC>(P);
-    uint8_t *sA = smem;                                  // thermometer table
-    uint8_t *sB = smem + Fp4Geom<JPF>::TAB;              // stream table(s)
+    uint8_t *sB = smem;                                  // stream table(s)
     constexpr int TR = WA * BA * 32, TC = WB * BB * 32;   // tile rows / columns
-    static_assert(5 * TR + 3 * TC <= kFactorFloats, "epilogue factor area too small");
+    static_assert(5 * TR + 3 * TC + 1 <= kFactorFloats, "epilogue factor area too small");
     float *s_rowf = (float *)(smem + ((tabs + 15) & ~15)); // [3][TR] sa, za, suma
     float *s_colf = s_rowf + 3 * TR;                     // [3][TC] sb, zb, sumb
     int64_t *s_rowo = (int64_t *)(s_colf + 3 * TC);      // [TR] output row offsets
+    // the finisher flag lives in the dynamic area too: with no static LDS the tables start
+    // at LDS address 0, and a table row's address is its scaled code alone
+    int &s_last = *(int *)(s_rowo + TR);
 
     fp4_load_tables<JPF, LUTSRC, NT>(P, sA, sB);
     __syncthreads();
@@ -688,8 +705,8 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
     constexpr int NT = 64 * WA * WB;
     constexpr int TR = WA * BA * 32, TC = WB * BB * 32;   // tile rows / columns
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    uint8_t *sA = smem;
-    uint8_t *sB = smem + Fp4Geom<JPF>::TAB;
+    __shared__ __attribute__((aligned(16))) uint8_t sA[Fp4Geom<JPF>::TAB];  // thermometer
+    uint8_t *sB = smem;
     const int tid = threadIdx.x;
     const int ta = blockIdx.x % P.tilesA, tb = blockIdx.x / P.tilesA;
     const int batch = blockIdx.z;
@@ -804,8 +821,13 @@ sc_gemm_fp4_chunked_kernel(GemmP P) {
 constexpr int kFp4MaxLds = 160 * 1024;
 
 template <class K>
-static int fp4_set_lds(K kern, size_t lds) {
-    if (lds <= 64 * 1024) return SCMP_OK;
+static int fp4_set_lds(K kern, size_t lds, size_t static_lds) {
+    if (lds + static_lds <= 64 * 1024) return SCMP_OK;
+    if (lds + static_lds > (size_t)kFp4MaxLds) {
+        set_error("scmp_sc_gemm(mfma fp4): %zu + %zu bytes of LDS exceed %d", lds, static_lds,
+                  kFp4MaxLds);
+        return SCMP_E_ARG;
+    }
     hipError_t e = hipFuncSetAttribute((const void *)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) {
@@ -816,12 +838,13 @@ static int fp4_set_lds(K kern, size_t lds) {
     return SCMP_OK;
 }
 
+// dynamic LDS of the stream tables (the thermometer table, Fp4Geom<JPF>::TAB bytes, is static)
 template <int JPF, int LUTSRC>
 static size_t fp4_tables_bytes_host(const GemmP &P) {
     using G = Fp4Geom<JPF>;
-    return (size_t)G::TAB * (1 + (LUTSRC == LUT_LDS || LUTSRC == LUT_RUNS ? 1
-                                  : LUTSRC == LUT_LDS_CLASSES                ? P.nclass
-                                                                             : 0));
+    return (size_t)G::TAB * (LUTSRC == LUT_LDS || LUTSRC == LUT_RUNS ? 1
+                             : LUTSRC == LUT_LDS_CLASSES                ? P.nclass
+                                                                        : 0);
 }
 
 // Non-chunked, tile shape SHAPE (waves of 4 x 4 blocks of 32 x 32, narrow: 2 x 2);
@@ -840,7 +863,7 @@ static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
     auto kern = sc_gemm_fp4_kernel<JPF, BA, BB, WA, WB, LUTSRC, SCHED>;
     const size_t lds = ((fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15) +
                        (size_t)kFactorFloats * sizeof(float);
-    int rc = fp4_set_lds(kern, lds);
+    int rc = fp4_set_lds(kern, lds, Fp4Geom<JPF>::TAB);
     if (rc != SCMP_OK) return rc;
     kern<<<dim3((unsigned)P.nwg), 64 * WA * WB, lds, stream>>>(P);
     SCMP_LAUNCH_CHECK("scmp_sc_gemm(mfma fp4)");
@@ -857,11 +880,11 @@ static int launch_fp4_chunked_rows(const GemmP &P0, int64_t batch, hipStream_t s
     const int64_t tilesB = cdiv(P.M, WB * BB * 32);
     const size_t tabs = (fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15;
     const size_t scales = (size_t)cdiv(P.D, P.chunk) * (WA * BA * 32 + WB * BB * 32) * sizeof(float);
-    const bool slds = tabs + scales <= (size_t)kFp4MaxLds;
+    const bool slds = Fp4Geom<JPF>::TAB + tabs + scales <= (size_t)kFp4MaxLds;
     auto kern = slds ? sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC, true>
                      : sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC, false>;
     const size_t lds = slds ? tabs + scales : tabs;
-    int rc = fp4_set_lds(kern, lds);
+    int rc = fp4_set_lds(kern, lds, Fp4Geom<JPF>::TAB);
     if (rc != SCMP_OK) return rc;
     kern<<<dim3((unsigned)(P.tilesA * tilesB), 1, (unsigned)batch), 64 * WA * WB, lds,
            stream>>>(P);
