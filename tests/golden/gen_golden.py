@@ -8,7 +8,7 @@ Run in the build container only (the reference is not present on the GPU box):
 What is run and why: the reference's fused Triton quantizers, its float64 host scale path
 and the per-path fp32 epilogue order are pinned by no closed form; these vectors pin the
 oracle's restatement of them. Two harness adaptations are needed for a GPU-less
-interpreter run (both are documented in DESIGN.md):
+interpreter run:
 
 * ``libdevice.nearbyint`` is not implemented by this Triton's interpreter; it is replaced
   by a round-half-to-even written in ``tl`` ops (same function on every input);
