@@ -42,6 +42,10 @@ struct GemmP {
     const int64_t *row_map;   // output row of A row n (NULL: n)
     const int32_t *group_class;   // FP4: class of each 8-d group (NULL: none)
     int row0;                 // chunked FP4 launch: first A row it computes
+    // FP4 split tiles: 0 = the last contributor to arrive adds the others' partial sums and
+    // applies the epilogue; 1 = every contributor publishes its partial sums and a fixup
+    // launch after the GEMM finishes the shared tiles (no counters)
+    int deferred;
 };
 
 // Output row of A row n: the caller's row map scatters a row subset in place.

@@ -112,13 +112,21 @@ int gemm_fp4_run(GemmP &P, const scmp_gemm_args &a, bool chunked, hipStream_t st
     P.ntiles = plan.ntiles;
     P.part = nullptr;
     P.cnt = nullptr;
+    P.deferred = 0;
     P.nwg = (int)plan.ntiles;                 // whole tiles unless the workspace allows splits
     if (plan.split && a.workspace && a.workspace_bytes >= plan.cnt_bytes + plan.part_bytes) {
         P.nwg = plan.nwg;
         P.cnt = (int *)a.workspace;
         P.part = (float *)((uint8_t *)a.workspace + plan.cnt_bytes);
-        zero_ints_kernel<<<cdiv(plan.ntiles, 256), 256, 0, stream>>>(P.cnt, plan.ntiles);
-        SCMP_LAUNCH_CHECK("scmp_sc_gemm(fp4 counters)");
+        // Fewer tiles than workgroups: most tiles have three or more contributors, which all
+        // finish at the end of the launch, so the last to arrive would add two or more slots
+        // and drain the tile while the rest of the chip idles. Those tiles are finished by a
+        // second launch over every compute unit instead (no counters).
+        P.deferred = plan.ntiles < plan.nwg ? 1 : 0;
+        if (!P.deferred) {
+            zero_ints_kernel<<<cdiv(plan.ntiles, 256), 256, 0, stream>>>(P.cnt, plan.ntiles);
+            SCMP_LAUNCH_CHECK("scmp_sc_gemm(fp4 counters)");
+        }
     } else if (!plan.split) {
         P.nwg = plan.nwg;                     // an even share of whole tiles each
     }

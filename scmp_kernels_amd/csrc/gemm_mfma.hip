@@ -492,6 +492,7 @@ extern "C" int scmp_sc_gemm(const scmp_gemm_args *args, hipStream_t stream) {
     P.row_map = a.row_map;
     P.group_class = a.group_class;
     P.row0 = 0;
+    P.deferred = 0;
     P.tilesA = 0;
     P.tile_cols = 256;
     P.nclass = a.nclass;
