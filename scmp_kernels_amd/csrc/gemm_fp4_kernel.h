@@ -705,67 +705,82 @@ sc_gemm_fp4_kernel(GemmP P) {
     }
 }
 
-// Deferred split tiles (P.deferred): after the persistent launch, workgroup (c, blk) of
-// this launch finishes block blk of the tile in which workgroup c's share of the work list
-// starts, when that start lies inside a tile and no lower workgroup's start lies in the same
-// tile (each shared tile is taken once, by its first inner boundary). Block blk is the
-// 32 x 32 block (i, cb) of wave w in the persistent kernel's partial-sum slot layout; thread
-// tid holds its quarter q = tid / 64 and lane, 4 values: the sum over the tile's
-// contributors' slots (exact integers), then the epilogue, stored like the fused drain.
-// Every workgroup of the persistent launch is a contributor of at most two tiles, so this
-// launch has (nwg - 1) x (blocks per tile) workgroups, most of which return at once.
+// Deferred split tiles (P.deferred): after the persistent launch, workgroup (t, blk) of
+// this launch finishes block blk of tile t when the tile was shared (its contributors are
+// the workgroups whose shares of the work list overlap it; a tile that one workgroup did
+// whole was drained by that workgroup). Block blk is the 32 x 32 block (i, cb) of wave w in
+// the persistent kernel's partial-sum slot layout; thread tid holds its quarter q = tid / 64
+// and lane, 4 values: the sum over the contributors' slots (exact integers), then the
+// epilogue, stored like the fused drain. Deferred launches have fewer tiles than
+// workgroups, so every schedule quantity fits 32 bits (W < 256 tiles x 8192 groups).
 template <int KIND, int BA, int BB, int WA, int WB>
 __global__ void __launch_bounds__(256) sc_gemm_fp4_fixup_kernel(GemmP P) {
     constexpr int NW = WA * WB, TILE_FLOATS = NW * BA * BB * 1024;
     constexpr int TR = WA * BA * 32, TC = WB * BB * 32;
-    const int64_t ngroups = (P.D + 7) / 8;
-    const int64_t W = P.ntiles * ngroups, nwg = P.nwg;
-    const int64_t c = (int64_t)blockIdx.x + 1;          // the boundary between c - 1 and c
-    const int64_t u = sched_first(c, W, nwg);
-    if (u % ngroups == 0) return;                       // falls on a tile start
-    const int64_t t = u / ngroups;
-    const int64_t cf = sched_owner(t * ngroups, W, nwg);
-    if (cf != c - 1) return;                            // a lower boundary takes this tile
-    const int64_t cl = sched_owner(t * ngroups + ngroups - 1, W, nwg);
+    const uint32_t ngroups = (uint32_t)(P.D + 7) / 8, nwg = (uint32_t)P.nwg;
+    const uint32_t W = (uint32_t)P.ntiles * ngroups;
+    const uint32_t t = blockIdx.x, tg = t * ngroups;
+    const uint32_t cf = ((tg + 1) * nwg - 1) / W;                   // owner of the tile start
+    const uint32_t cl = ((tg + ngroups) * nwg - 1) / W;             // owner of its last group
+    if (cf == cl) return;                                           // a whole tile
+    // contributor cf's segment is its first one only when its share starts at the tile;
+    // every later contributor's share starts inside the tile (slot 2c, as in fp4_slot)
+    const uint32_t slot_cf = 2 * cf + (cf * W / nwg == tg ? 0u : 1u);
     const int blk = blockIdx.y;                         // ((w * BA + i) * BB + cb)
     const int w = blk / (BA * BB), i = (blk / BB) % BA, cb = blk % BB;
     const int tid = threadIdx.x, q = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, li = lane & 31;
     const int64_t off = (int64_t)blk * 1024 + q * 256 + lane * 4;
-    v4f sum = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int64_t c2 = cf; c2 <= cl; ++c2) {
-        const v4f v = *(const v4f *)(P.part + fp4_slot(c2, t, W, nwg, (int)ngroups) *
-                                                  (int64_t)TILE_FLOATS + off);
-        sum += v;                                       // integers below 2^24: exact
-    }
-    const int64_t tiles_per_batch = (int64_t)P.tilesA * P.tilesB;
+    const uint32_t tiles_per_batch = (uint32_t)P.tilesA * (uint32_t)P.tilesB;
     const int64_t batch = t / tiles_per_batch;
-    const int64_t rem = t - batch * tiles_per_batch;
-    const int ta = (int)(rem % P.tilesA), tb = (int)(rem / P.tilesA);
+    const uint32_t rem = t - (uint32_t)batch * tiles_per_batch;
+    const int ta = (int)(rem % (uint32_t)P.tilesA), tb = (int)(rem / (uint32_t)P.tilesA);
     const int wa = w % WA, wb = w / WA;
-    const int m = tb * TC + (wb * BB + cb) * 32 + li;
-    if (m >= P.M) return;
+    const int mraw = tb * TC + (wb * BB + cb) * 32 + li;
     const int nb = ta * TR + (wa * BA + i) * 32 + 8 * q + 4 * h;   // rows nb .. nb + 3
-    const int64_t ybase = batch * P.bsy;
+    // every load issued before any is used (none under a branch: indices clamped, values
+    // past N or M are computed and not stored)
+    const int m = mraw < P.M ? mraw : P.M - 1;
+    int64_t orow[4];
+    float rf[4][3];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int n = nb + e < P.N ? nb + e : P.N - 1;
+        orow[e] = out_row(P.row_map, n);
+        if (KIND != SCMP_EPI_INT) epi_row_factors(P.epi, n, batch, rf[e]);
+    }
     float cf3[3] = {0.f, 0.f, 0.f};
     EpiUniform eu = {0.f, 0.f, 0.f, 0.f};
     if (KIND != SCMP_EPI_INT) {
         epi_col_factors(P.epi, m, batch, cf3);
         eu = epi_uniform(P.epi, batch);
     }
+    // the contributors' slots, four at a time with all four loads in flight
+    constexpr int KS = 4;
+    v4f sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t c0 = cf; c0 <= cl; c0 += KS) {
+        v4f v[KS];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const uint32_t c2 = c0 + k <= cl ? c0 + k : cl;
+            const uint32_t slot = c2 == cf ? slot_cf : 2 * c2;
+            v[k] = *(const v4f *)(P.part + (int64_t)slot * TILE_FLOATS + off);
+        }
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+            if (c0 + k <= cl) sum += v[k];              // integers below 2^24: exact
+    }
+    if (mraw >= P.M) return;
+    const int64_t ybase = batch * P.bsy;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const int n = nb + e;
-        if (n >= P.N) break;
-        const int64_t o = ybase + out_row(P.row_map, n) * P.ldy + m;
-        if (KIND == SCMP_EPI_INT) {
+        if (nb + e >= P.N) break;
+        const int64_t o = ybase + orow[e] * P.ldy + m;
+        if (KIND == SCMP_EPI_INT)
             P.iout[o] = (int32_t)sum[e];
-        } else {
-            float rf[3];
-            epi_row_factors(P.epi, n, batch, rf);
-            P.y[o] = epilogue_apply_k<KIND>(P.epi, sum[e], rf[0], rf[1], rf[2], cf3[0], cf3[1],
-                                            cf3[2], eu);
-        }
+        else
+            P.y[o] = epilogue_apply_k<KIND>(P.epi, sum[e], rf[e][0], rf[e][1], rf[e][2], cf3[0],
+                                            cf3[1], cf3[2], eu);
     }
 }
 
@@ -938,7 +953,7 @@ static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
     kern<<<dim3((unsigned)P.nwg), 64 * WA * WB, lds, stream>>>(P);
     SCMP_LAUNCH_CHECK("scmp_sc_gemm(mfma fp4)");
     if (P.deferred && P.nwg > 1) {
-        const dim3 grid((unsigned)(P.nwg - 1), (unsigned)(WA * WB * BA * BB));
+        const dim3 grid((unsigned)P.ntiles, (unsigned)(WA * WB * BA * BB));
         switch (P.epi.kind) {
         case SCMP_EPI_INT:
             sc_gemm_fp4_fixup_kernel<SCMP_EPI_INT, BA, BB, WA, WB><<<grid, 256, 0, stream>>>(P);
