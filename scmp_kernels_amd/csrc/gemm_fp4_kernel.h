@@ -104,6 +104,34 @@ __device__ __forceinline__ void interleave_unit() {
     }
 }
 
+// Front-loaded interleave of one unit: MFMA k is followed by VPK VALU instructions until NVT
+// are placed, and by DPK LDS reads from MFMA DS0 on, so the next unit's address arithmetic
+// and table reads are issued in the first MFMAs of the unit and their results arrive well
+// before the next unit's MFMAs need them.
+template <int K, int NM, int NDS, int NVT, int VPK, int DPK, int DS0>
+__device__ __forceinline__ void interleave_front() {
+    if constexpr (K < NM) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
+        constexpr int vd = K * VPK;
+        if constexpr (vd < NVT)
+            __builtin_amdgcn_sched_group_barrier(0x002, (NVT - vd) < VPK ? (NVT - vd) : VPK, 0);
+        constexpr int dd = (K - DS0) * DPK;
+        if constexpr (K >= DS0 && dd < NDS)
+            __builtin_amdgcn_sched_group_barrier(0x100, (NDS - dd) < DPK ? (NDS - dd) : DPK, 0);
+        interleave_front<K + 1, NM, NDS, NVT, VPK, DPK, DS0>();
+    }
+}
+
+// The pinned schedule of one unit (NM MFMAs, NDS LDS reads of the next unit): one read and
+// two VALU slots per MFMA for JPF >= 128; front-loaded for JPF = 64 (about 22 VALU per unit)
+// and JPF = 16 (about 52).
+template <int JPF, int NM, int NDS>
+__device__ __forceinline__ void interleave_pinned() {
+    if constexpr (JPF >= 128) interleave_unit<NM, NDS, 2>();
+    else if constexpr (JPF == 64) interleave_front<0, NM, NDS, 22, 4, 2, 2>();
+    else interleave_front<0, NM, NDS, 52, 6, 2, 1>();
+}
+
 // LDS layout of both kernels: the thermometer table is a static array (its address is a
 // compile-time constant, so a lookup's address is its scaled code with the base in the
 // read's offset field), then the dynamic area [stream table(s) | epilogue factors].
@@ -185,8 +213,6 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
     constexpr int ROWB = G::ROWB, KSU = G::KSU, SPD = G::SPD, UPG = G::UPG, LS = G::LS,
                   TAB = G::TAB;
     constexpr int NR = BA + BB;                  // code rows per lane: A rows, then B rows
-    // VALU slots per MFMA in the pinned interleave (two for JPF >= 128: 0.4% at cfg2)
-    constexpr int NVS = JPF >= 128 ? 2 : 1;
     constexpr bool PERD = LUTSRC == LUT_LDS_CLASSES || LUTSRC == LUT_GLOBAL;   // per-d classes
     const uint8_t *glut = (const uint8_t *)P.lut;
     const int D = P.D;
@@ -378,7 +404,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             stage(F1, ca, cls, qb, m, uu + 1, dg);
             mma(F0);
             if (SCHED) {
-                interleave_unit<BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1), NVS>();
+                interleave_pinned<JPF, BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1)>();
                 __builtin_amdgcn_sched_barrier(0);
             }
             done(uu, dg);
@@ -394,7 +420,7 @@ __device__ __forceinline__ void fp4_accumulate(const GemmP &P, const uint8_t *sA
             }
             mma(F1);
             if (SCHED) {
-                interleave_unit<BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1), NVS>();
+                interleave_pinned<JPF, BA * BB * KSU, NR * KSU * (JPF == 16 ? 2 : 1)>();
                 __builtin_amdgcn_sched_barrier(0);
             }
             done(uu + 1, dg);
@@ -942,9 +968,9 @@ static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
                   WA = NARROW ? 4 : SHAPE == TILE_WIDE ? 1 : 2,
                   WB = NARROW ? 1 : SHAPE == TILE_WIDE ? 4 : 2;
     GemmP P = P0;
-    // MFMA / LDS-read interleaving pinned for JPF = 16 and >= 128; for 32 and 64 the
-    // compiler's own schedule measured 9.5% and 3.6% faster (pinned: 3.5% faster at 16)
-    constexpr bool SCHED = JPF == 16 || JPF >= 128;
+    // MFMA / LDS-read interleaving pinned for JPF = 16, 64 and >= 128; for JPF = 32 the
+    // compiler's own schedule measured 9.5% faster
+    constexpr bool SCHED = JPF != 32;
     auto kern = sc_gemm_fp4_kernel<JPF, BA, BB, WA, WB, LUTSRC, SCHED>;
     const size_t lds = ((fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15) +
                        (size_t)kFactorFloats * sizeof(float);
