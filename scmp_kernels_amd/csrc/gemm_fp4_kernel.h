@@ -92,19 +92,8 @@ struct Fp4Frag {
     v4i b[BB][Fp4Geom<JPF>::KSU];
 };
 
-// Interleave one unit's MFMAs with the next unit's LDS reads and address arithmetic:
-// per MFMA one DS read (while any remain) and NV VALU instructions.
-template <int NM, int NDS, int NV>
-__device__ __forceinline__ void interleave_unit() {
-#pragma unroll
-    for (int k = 0; k < NM; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
-        if (k < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-        __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);         // VALU
-    }
-}
-
-// Front-loaded interleave of one unit: MFMA k is followed by VPK VALU instructions until NVT
+// Interleave of one unit's MFMAs with the next unit's LDS reads and address arithmetic,
+// front-loaded: MFMA k is followed by VPK VALU instructions until NVT
 // are placed, and by DPK LDS reads from MFMA DS0 on, so the next unit's address arithmetic
 // and table reads are issued in the first MFMAs of the unit and their results arrive well
 // before the next unit's MFMAs need them.
@@ -122,14 +111,14 @@ __device__ __forceinline__ void interleave_front() {
     }
 }
 
-// The pinned schedule of one unit (NM MFMAs, NDS LDS reads of the next unit): one read and
-// two VALU slots per MFMA for JPF >= 128; front-loaded for JPF = 64 (about 22 VALU per unit)
-// and JPF = 16 (about 52).
+// The pinned schedule of one unit (NM MFMAs, NDS LDS reads of the next unit), front-loaded
+// with the VALU count of each table width's unit (about 24 at JPF >= 128, 22 at 64, 52 at
+// 16); the slots per MFMA were chosen by timing at cfg2 and cfg5.
 template <int JPF, int NM, int NDS>
 __device__ __forceinline__ void interleave_pinned() {
-    if constexpr (JPF >= 128) interleave_unit<NM, NDS, 2>();
+    if constexpr (JPF >= 128) interleave_front<0, NM, NDS, 24, 3, 1, 1>();
     else if constexpr (JPF == 64) interleave_front<0, NM, NDS, 22, 4, 2, 2>();
-    else interleave_front<0, NM, NDS, 52, 6, 2, 1>();
+    else interleave_front<0, NM, NDS, 52, 8, 2, 1>();
 }
 
 // LDS layout of both kernels: the thermometer table is a static array (its address is a
