@@ -462,54 +462,89 @@ __device__ __forceinline__ int64_t fp4_slot(int64_t c, int64_t t, int64_t W, int
     return 2 * c + (sched_first(c, W, nwg) / ngroups == t ? 0 : 1);
 }
 
-// Fused epilogue of a finished tile, stored straight from the accumulators. In the MFMA
-// layout lane (li, h) of block (i, c) holds row 32i + 8(r>>2) + 4h + (r&3) and column
-// 32c + li of the wave's quadrant, so for each register r the 32 lanes of a half store 32
-// consecutive values of one row. Row factors and output row offsets come from LDS (nrb:
-// the lane's tile-local row of i = r = 0), column factors once per block column (mcb, mb:
-// tile-local and global column of c = 0). Only stores reach global memory.
+// Per-wave staging area of the drain: one 32 x 32 block, rows kStageStride floats apart (the
+// two lane halves' rows, 4 apart, then fall on disjoint bank halves).
+constexpr int kStageStride = 40;
+constexpr int kStageFloats = 32 * kStageStride;          // per wave
+
+// four floats at a 4-byte aligned address (rows whose stride is not a multiple of 4
+// floats): one 16-byte store
+struct __attribute__((aligned(4))) f4u {
+    float x, y, z, w;
+};
+
+// Fused epilogue of a finished tile. In the MFMA layout lane (li, h) of block (i, c) holds
+// row 32i + 8(r>>2) + 4h + (r&3) and column 32c + li of the wave's quadrant; the epilogue is
+// applied there (row factors and output row offsets from LDS, column factors once per block
+// column), each block's values go through the wave's staging area in LDS, and lane L reads
+// back 4 consecutive columns 4(L & 7).. of rows (L >> 3) + 8k, so the tile leaves as 16-byte
+// stores (a quarter of the store instructions of one float per lane, which measured the
+// drain's bound); a group of columns that runs past M is stored value by value. Only
+// stores reach global memory (any load between them would make the wave wait for every
+// earlier store on gfx9).
 template <int KIND, int BA, int BB, int TR, int TC>
 __device__ __forceinline__ void fp4_drain(const GemmP &P, const v16f (&acc)[BA][BB],
                                           const float *s_rowf, const float *s_colf,
                                           const int64_t *s_rowo, const EpiUniform &eu,
-                                          int nrb, int mcb, int mb, int64_t ybase) {
+                                          float *stg, int lane, int nrw, int mcw, int tc0,
+                                          int64_t ybase) {
+    const int h = lane >> 5, li = lane & 31;
+    const int rq = lane >> 3, cq = 4 * (lane & 7);
     float cb[BB], cz[BB], cs[BB];
-    bool mok[BB];
 #pragma unroll
     for (int c = 0; c < BB; ++c) {
-        const int mc = mcb + 32 * c;
+        const int mc = mcw + 32 * c + li;
         cb[c] = s_colf[mc];
         cz[c] = s_colf[TC + mc];
         cs[c] = s_colf[2 * TC + mc];
-        mok[c] = mb + 32 * c < P.M;
     }
     constexpr bool ZP = KIND == SCMP_EPI_ZP_ROWCOL || KIND == SCMP_EPI_ZP_SCALAR;
     constexpr bool RA = KIND == SCMP_EPI_ROWCOL || KIND == SCMP_EPI_ZP_ROWCOL;
 #pragma unroll
     for (int i = 0; i < BA; ++i) {
-        // the 16 rows of this block row: offsets and factors first (one LDS wait), then
-        // the stores, predicated instead of branched around
-        int64_t ro[16];
         float ra[16], rz[16], rs[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int nr = nrb + 32 * i + 8 * (r >> 2) + (r & 3);
-            ro[r] = s_rowo[nr];
+            const int nr = nrw + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
             ra[r] = RA ? s_rowf[nr] : 0.f;
             rz[r] = KIND == SCMP_EPI_ZP_ROWCOL ? s_rowf[TR + nr] : 0.f;
             rs[r] = ZP ? s_rowf[2 * TR + nr] : 0.f;
         }
+        int64_t ro[4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t o = ybase + ro[r] + mb;
+        for (int k = 0; k < 4; ++k) ro[k] = s_rowo[nrw + 32 * i + rq + 8 * k];
 #pragma unroll
-            for (int c = 0; c < BB; ++c) {
-                if (ro[r] < 0 || !mok[c]) continue;          // row past N, column past M
-                if constexpr (KIND == SCMP_EPI_INT)
-                    P.iout[o + 32 * c] = (int32_t)acc[i][c][r];
-                else
-                    P.y[o + 32 * c] = epilogue_apply_k<KIND>(P.epi, acc[i][c][r], ra[r], rz[r],
+        for (int c = 0; c < BB; ++c) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float v = KIND == SCMP_EPI_INT
+                                    ? __int_as_float((int32_t)acc[i][c][r])
+                                    : epilogue_apply_k<KIND>(P.epi, acc[i][c][r], ra[r], rz[r],
                                                              rs[r], cb[c], cz[c], cs[c], eu);
+                stg[(8 * (r >> 2) + 4 * h + (r & 3)) * kStageStride + li] = v;
+            }
+            const int m = tc0 + mcw + 32 * c + cq;
+            const int nv = P.M - m;                           // valid columns from m
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const v4f v = *(const v4f *)(stg + (rq + 8 * k) * kStageStride + cq);
+                if (ro[k] < 0 || nv <= 0) continue;           // row past N, columns past M
+                const int64_t o = ybase + ro[k] + m;
+                if (nv >= 4) {
+                    if constexpr (KIND == SCMP_EPI_INT)
+                        *(f4u *)(P.iout + o) = f4u{v[0], v[1], v[2], v[3]};
+                    else
+                        *(f4u *)(P.y + o) = f4u{v[0], v[1], v[2], v[3]};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 3; ++e) {
+                        if (e >= nv) break;
+                        if constexpr (KIND == SCMP_EPI_INT)
+                            P.iout[o + e] = __float_as_int(v[e]);
+                        else
+                            P.y[o + e] = v[e];
+                    }
+                }
             }
         }
     }
@@ -533,6 +568,7 @@ sc_gemm_fp4_kernel(GemmP P) {
     // the finisher flag lives in the dynamic area too: with no static LDS the tables start
     // at LDS address 0, and a table row's address is its scaled code alone
     int &s_last = *(int *)(s_rowo + TR);
+    float *s_stage = s_rowf + kFactorFloats;             // [NW][kStageFloats] drain staging
 
     fp4_load_tables<JPF, LUTSRC, NT>(P, sA, sB);
     __syncthreads();
@@ -581,7 +617,6 @@ sc_gemm_fp4_kernel(GemmP P) {
         // out of the loop into registers that the main loop's pressure would spill.
         int lt = lane;
         asm volatile("" : "+v"(lt));
-        const int ecol = lt & 31, ehalf = lt >> 5;
         // partial-sum slot layout: block (i, c) of this wave, then the quarter q of the
         // lane's 16 accumulator registers, then lane (4 floats each): one 16-byte access per
         // lane covers 1 KB of consecutive memory
@@ -689,30 +724,27 @@ sc_gemm_fp4_kernel(GemmP P) {
             }
             const EpiUniform eu = fp32 ? epi_uniform(P.epi, batch) : EpiUniform{0.f, 0.f, 0.f, 0.f};
             __syncthreads();
-            const int nrb = wa * (BA * 32) + 4 * ehalf;
-            const int mcb = wb * (BB * 32) + ecol;
-            const int mb = tc0 + mcb;
+            const int nrw = wa * (BA * 32), mcw = wb * (BB * 32);
+            float *stg = s_stage + wave * kStageFloats;
             const int64_t ybase = batch * P.bsy;
             switch (P.epi.kind) {
             case SCMP_EPI_INT:
-                fp4_drain<SCMP_EPI_INT, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                fp4_drain<SCMP_EPI_INT, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, stg, lt, nrw, mcw, tc0, ybase);
                 break;
             case SCMP_EPI_ROWCOL:
-                fp4_drain<SCMP_EPI_ROWCOL, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                fp4_drain<SCMP_EPI_ROWCOL, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, stg, lt, nrw, mcw, tc0, ybase);
                 break;
             case SCMP_EPI_SCALAR:
-                fp4_drain<SCMP_EPI_SCALAR, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                fp4_drain<SCMP_EPI_SCALAR, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, stg, lt, nrw, mcw, tc0, ybase);
                 break;
             case SCMP_EPI_HEAD:
-                fp4_drain<SCMP_EPI_HEAD, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb, ybase);
+                fp4_drain<SCMP_EPI_HEAD, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, stg, lt, nrw, mcw, tc0, ybase);
                 break;
             case SCMP_EPI_ZP_ROWCOL:
-                fp4_drain<SCMP_EPI_ZP_ROWCOL, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb,
-                                              ybase);
+                fp4_drain<SCMP_EPI_ZP_ROWCOL, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, stg, lt, nrw, mcw, tc0, ybase);
                 break;
             default:
-                fp4_drain<SCMP_EPI_ZP_SCALAR, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, nrb, mcb, mb,
-                                              ybase);
+                fp4_drain<SCMP_EPI_ZP_SCALAR, BA, BB, TR, TC>(P, acc, s_rowf, s_colf, s_rowo, eu, stg, lt, nrw, mcw, tc0, ybase);
                 break;
             }
         }
@@ -962,7 +994,7 @@ static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
     constexpr bool SCHED = JPF != 32;
     auto kern = sc_gemm_fp4_kernel<JPF, BA, BB, WA, WB, LUTSRC, SCHED>;
     const size_t lds = ((fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15) +
-                       (size_t)kFactorFloats * sizeof(float);
+                       (size_t)(kFactorFloats + WA * WB * kStageFloats) * sizeof(float);
     int rc = fp4_set_lds(kern, lds, Fp4Geom<JPF>::TAB);
     if (rc != SCMP_OK) return rc;
     kern<<<dim3((unsigned)P.nwg), 64 * WA * WB, lds, stream>>>(P);
@@ -1064,7 +1096,7 @@ int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t
     using Classes = std::integral_constant<int, LUT_LDS_CLASSES>;
     using Global = std::integral_constant<int, LUT_GLOBAL>;
     using Runs = std::integral_constant<int, LUT_RUNS>;
-    const int64_t stage = kFactorFloats * (int64_t)sizeof(float);
+    const int64_t stage = (kFactorFloats + 4 * kStageFloats) * (int64_t)sizeof(float);
     if (P.group_class != nullptr) {
         if (chunked || P.d_class != nullptr || P.nclass <= 0) {
             set_error("scmp_sc_gemm(fp4): group_class needs a non-chunked launch, no d_class "
