@@ -529,6 +529,21 @@ def test_per_head_vs_oracle(shape):
     bits_equal(y, O.sc_matmul(q, k, "per_head"))
 
 
+@pytest.mark.parametrize("shape", [(600, 197, 197, 64), (300, 96, 384, 96), (260, 40, 900, 40)])
+def test_per_head_many_large_heads(shape):
+    """More heads than compute units, heads of 64 to 155 KB of fp32 (P-like 197 x 197;
+    rows of 96 or 225 four-column chunks; 4-aligned and ragged rows): sampled heads (first,
+    last, middle, and those past the first 256 and 512) against the oracle."""
+    from scmp_kernels_amd import sc_matmul
+    BH, N, D, M = shape
+    rng = np.random.default_rng(BH + N + D)
+    q = rng.standard_normal((BH, N, D)).astype(np.float32)
+    k = rng.standard_normal((BH, M, D)).astype(np.float32)
+    y = sc_matmul(T(q), T(k), "per_head")
+    heads = sorted({0, 1, BH // 2, BH - 2, BH - 1, 256, 257, 511 % BH})
+    bits_equal(y[heads], O.sc_matmul(q[heads], k[heads], "per_head"))
+
+
 def test_per_row_3d_wide_tiles_vs_oracle():
     """Batched operands whose per-batch output (300 x 500) takes 128 x 512 tiles."""
     from scmp_kernels_amd import sc_matmul
