@@ -589,14 +589,30 @@ sc_gemm_fp4_kernel(GemmP P) {
                                ? (blockIdx.x % kXcds) * (nwg / kXcds) + blockIdx.x / kXcds
                                : (int64_t)blockIdx.x;
     const int64_t u_end = sched_first(c_self + 1, W, nwg);
+    // work lists below 2^31 items (every practical launch) index tiles in 32-bit arithmetic
+    const bool w32 = W < ((int64_t)1 << 31);
 
     for (int64_t u = sched_first(c_self, W, nwg); u < u_end;) {
-        const int64_t t = u / ngroups;
-        const int g0 = (int)(u - t * ngroups);
+        int64_t t, batch;
+        int g0, ta, tb;
+        if (w32) {
+            const uint32_t ng = (uint32_t)ngroups, t32 = (uint32_t)u / ng;
+            const uint32_t tpb = (uint32_t)tiles_per_batch, b32 = t32 / tpb;
+            const uint32_t rem = t32 - b32 * tpb, tA = (uint32_t)P.tilesA;
+            t = t32;
+            batch = b32;
+            g0 = (int)((uint32_t)u - t32 * ng);
+            ta = (int)(rem % tA);
+            tb = (int)(rem / tA);
+        } else {
+            t = u / ngroups;
+            g0 = (int)(u - t * ngroups);
+            batch = t / tiles_per_batch;
+            const int64_t rem = t - batch * tiles_per_batch;
+            ta = (int)(rem % P.tilesA);
+            tb = (int)(rem / P.tilesA);
+        }
         const int g1 = (int)(u_end - t * ngroups < ngroups ? u_end - t * ngroups : ngroups);
-        const int64_t batch = t / tiles_per_batch;
-        const int64_t rem = t - batch * tiles_per_batch;
-        const int ta = (int)(rem % P.tilesA), tb = (int)(rem / P.tilesA);
         const int a0 = (ta * WA + wa) * (BA * 32);
         const int b0 = (tb * WB + wb) * (BB * 32);
 
@@ -609,6 +625,10 @@ sc_gemm_fp4_kernel(GemmP P) {
         for (int i = 0; i < BA; ++i)
 #pragma unroll
             for (int c = 0; c < BB; ++c) acc[i][c] = (v16f){0.0f};
+        // the tile-uniform epilogue values (the head's scales of a per-head product), loaded
+        // now so that their latency passes under the first code loads, not at the drain
+        const bool fp32 = P.epi.kind != SCMP_EPI_INT;
+        const EpiUniform eu = fp32 ? epi_uniform(P.epi, batch) : EpiUniform{0.f, 0.f, 0.f, 0.f};
         fp4_accumulate<JPF, BA, BB, LUTSRC, SCHED>(P, sA, sB, abase, bbase, li, g0, g1, h, acc,
                                                     [](int, int) {});
 
@@ -700,7 +720,6 @@ sc_gemm_fp4_kernel(GemmP P) {
             // the tile's epilogue factors, once: row factors of its TR rows and column
             // factors of its TC columns into LDS, the uniform ones into registers
             const int tr0 = ta * TR, tc0 = tb * TC;
-            const bool fp32 = P.epi.kind != SCMP_EPI_INT;
             __syncthreads();          // every wave is past the previous tile's last store
             // where each row of the tile goes (row map applied, times ldy; -1 past N): the
             // drain below then issues no loads, so no store ever waits for another
@@ -722,7 +741,6 @@ sc_gemm_fp4_kernel(GemmP P) {
                     s_colf[2 * TC + e] = f[2];
                 }
             }
-            const EpiUniform eu = fp32 ? epi_uniform(P.epi, batch) : EpiUniform{0.f, 0.f, 0.f, 0.f};
             __syncthreads();
             const int nrw = wa * (BA * 32), mcw = wb * (BB * 32);
             float *stg = s_stage + wave * kStageFloats;
