@@ -302,6 +302,7 @@ constexpr int kGroupThreads = 256;
 constexpr int kGroupMaxRows = 1024;       // row sums of a group live in LDS
 constexpr int kMaxChunks = 16;            // register-held 4-column chunks per thread, max
 constexpr int kBigGroupThreads = 1024;    // threads of a workgroup for groups past 256 x 16
+constexpr int kMidGroupThreads = 512;     // wide groups when 1024 threads would need 2 rounds
 constexpr int kBigChunks = 12;            // register-held chunks per thread at 1024 threads
                                           // (128 registers: 16 would spill)
 
@@ -419,7 +420,7 @@ __device__ __forceinline__ void zero_pad_share(const scmp_quant_args &a, int64_t
 
 // PT: register-held chunks per thread (npt <= PT); npt > PT re-reads the chunks instead.
 template <int OP, int SM, int PT, int NT>
-__global__ void __launch_bounds__(NT)
+__global__ void __launch_bounds__(NT, NT == kMidGroupThreads ? 4 : 1)
 quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt) {
     __shared__ uint32_t red0[NT / 64], red1[NT / 64];
     __shared__ float rsums[kGroupMaxRows];
@@ -788,7 +789,7 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt) {
 // 4, 16-byte aligned; no row index; no group across a batch): chunk k of a thread is chunk
 // tid + k * NT of the group in both buffers, so its addresses are fixed offsets.
 template <int OP, int PT, int NT, int CODE, bool SUM, bool SMOOTH, bool DENSE>
-__global__ void __launch_bounds__(NT)
+__global__ void __launch_bounds__(NT, NT == kMidGroupThreads ? 4 : 1)
 quant_codes_kernel(scmp_quant_args a, int G, int cpr, int npt) {
     __shared__ uint32_t red0[NT / 64], red1[NT / 64];
     __shared__ float rsums[SUM ? kGroupMaxRows : 1];
@@ -1066,16 +1067,19 @@ static void launch_codes(const scmp_quant_args &a, dim3 grid, int G, int cpr, in
 // codes, row sums exactly for the zero-point variant, every chunk in registers); false:
 // not covered.
 template <int OP>
-static bool try_codes(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt, bool wide,
+static bool try_codes(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt, int wide,
                       hipStream_t stream) {
     if (!a.code || a.beta16 || a.beta32 || a.sign || a.xint || a.cols < 4) return false;
     if (a.code_kind == SCMP_CODE_THERMO && a.col_class != nullptr) return false;
     if ((a.rowsum != nullptr) != (OP == QOP_DIVZP)) return false;
     const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
     if (cbr % G != 0 && cbr < a.rows) return false;      // a group across a batch boundary
-    if (wide) {
+    if (wide == 1) {
         launch_codes<OP, 4, kBigGroupThreads>(a, grid, G, cpr,
                                               (int)cdiv((int64_t)G * cpr, kBigGroupThreads), stream);
+    } else if (wide == 2) {
+        launch_codes<OP, 8, kMidGroupThreads>(a, grid, G, cpr,
+                                              (int)cdiv((int64_t)G * cpr, kMidGroupThreads), stream);
     } else if (npt <= 4) {
         launch_codes<OP, 4, kGroupThreads>(a, grid, G, cpr, npt, stream);
     } else if (npt <= kMaxChunks) {
@@ -1322,13 +1326,19 @@ static void launch_group_pt(const scmp_quant_args &a, dim3 grid, int G, int cpr,
 // A group too large for 256 threads' registers takes 1024 threads (multiply-by-reciprocal
 // variants: the per-head attention operands, one group per head), so it is read once.
 // `wide`: few groups of 1025 to 4096 chunks (a row subset of a mixed-precision level)
-// also take 1024 threads, four times the loads in flight per group.
+// also take more threads, more loads in flight per group: 1024 (wide 1) when the groups fit
+// the compute units once, else 512 (wide 2), two workgroups per compute unit, so that every
+// group is in flight at once.
 template <int OP>
 static void launch_group(const scmp_quant_args &a, dim3 grid, int G, int cpr, int npt,
-                         bool wide, hipStream_t stream) {
-    if (wide) {
+                         int wide, hipStream_t stream) {
+    if (wide == 1) {
         launch_group_pt<OP, 4, kBigGroupThreads>(a, grid, G, cpr,
                                                  (int)cdiv((int64_t)G * cpr, kBigGroupThreads),
+                                                 stream);
+    } else if (wide == 2) {
+        launch_group_pt<OP, 8, kMidGroupThreads>(a, grid, G, cpr,
+                                                 (int)cdiv((int64_t)G * cpr, kMidGroupThreads),
                                                  stream);
     } else if (npt <= 4) {
         launch_group_pt<OP, 4>(a, grid, G, cpr, npt, stream);
@@ -1360,9 +1370,13 @@ static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stre
     const int64_t ngroups = cdiv(a.rows, G);
     const int64_t cpr = cdiv(a.cols, 4);
     // fewer than two 256-thread workgroups per compute unit, each group one to four chunks
-    // per thread at 1024 threads
-    const bool wide = ngroups < 2 * (int64_t)quant_cu_count() && G * cpr > kBigGroupThreads &&
-                      G * cpr <= 4 * (int64_t)kBigGroupThreads;
+    // per thread at 1024 threads (or two to eight at 512, when there are more groups than
+    // compute units)
+    const int64_t ncu = quant_cu_count();
+    const int wide = ngroups < 2 * ncu && G * cpr > kBigGroupThreads &&
+                             G * cpr <= 4 * (int64_t)kBigGroupThreads
+                         ? (ngroups > ncu ? 2 : 1)
+                         : 0;
     const int64_t per = cdiv(G * cpr, kGroupThreads);
     const dim3 grid((unsigned)ngroups);
     const int npt = (int)(per <= kMaxChunks ? per : kMaxChunks + 1);   // at 256 threads

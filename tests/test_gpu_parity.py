@@ -309,6 +309,35 @@ def test_quant_codes_ragged_columns_and_padding(asym, cols, rows, G, cbr):
                                       ref_q.astype(np.float64).sum(axis=1).astype(np.float32))
 
 
+@pytest.mark.parametrize("asym", [False, True])
+@pytest.mark.parametrize("rows", [1368, 1000])
+def test_quant_codes_wide_groups(asym, rows):
+    """Row groups of 4 x 4096 (4096 four-column chunks), more groups than compute units
+    (1368 rows: 342 groups, 512-thread workgroups two per compute unit) and fewer (1000
+    rows: 250 groups, 1024-thread workgroups): code bytes and row sums against the
+    oracle."""
+    from scmp_kernels_amd import _lib
+    from scmp_kernels_amd.sc import kernels as K
+    G, cols = 4, 4096
+    Q = 255 if asym else 127
+    x = np.random.default_rng(rows + asym).standard_normal((rows, cols)).astype(np.float32)
+    if asym:
+        _, _, ref_q = O.grouped_asym(x, G, Q)
+    else:
+        _, ref_q, _ = O.grouped_sym(x, G, Q)
+    ref = (ref_q.astype(np.int32) & 0xff).astype(np.uint8)
+    code = torch.full((rows, cols), 0x5A, dtype=torch.uint8, device=_dev())
+    rs = torch.full((rows,), -1.0, dtype=torch.float32, device=_dev()) if asym else None
+    ws = K.quantize(T(x), _lib.Q_GROUP_ASYM if asym else _lib.Q_GROUP_SYM, Q, 256, group=G,
+                    code=code, code_kind=_lib.CODE_Q, rowsum=rs)
+    got = code.cpu().numpy()
+    del ws
+    np.testing.assert_array_equal(got, ref)
+    if asym:
+        np.testing.assert_array_equal(rs.cpu().numpy(),
+                                      ref_q.astype(np.float64).sum(axis=1).astype(np.float32))
+
+
 # -------------------------------------------------------------------------------------
 # the SC GEMM: integer accumulator against the oracle
 # -------------------------------------------------------------------------------------
