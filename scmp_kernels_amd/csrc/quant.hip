@@ -305,6 +305,7 @@ constexpr int kBigGroupThreads = 1024;    // threads of a workgroup for groups p
 constexpr int kMidGroupThreads = 512;     // wide groups when 1024 threads would need 2 rounds
 constexpr int kBigChunks = 12;            // register-held chunks per thread at 1024 threads
                                           // (128 registers: 16 would spill)
+constexpr int kMidChunks = 20;            // at 512 threads, two workgroups per compute unit
 
 enum { QOP_DIV = 0, QOP_DIVZP = 1, QOP_MUL = 2 };
 
@@ -954,8 +955,11 @@ quant_codes_kernel(scmp_quant_args a, int G, int cpr, int npt) {
         // DENSE: the group's first code row (r0's batch and row within it)
         const int64_t gb = r0 / cbr;
         uint32_t *cg = (uint32_t *)(a.code + (gb * a.code_rows + (r0 - gb * cbr)) * a.code_ld);
+        // the pass restarts from an opaque copy of the first position, so the chunk
+        // offsets are recomputed here instead of kept in registers from the first pass
         int rr = rr_first, cc = cc_first;
-        uint32_t xo = 0, co = (uint32_t)rr_first * cld32 + 4u * (uint32_t)cc_first;
+        asm volatile("" : "+v"(rr), "+v"(cc));
+        uint32_t xo = 0, co = (uint32_t)rr * cld32 + 4u * (uint32_t)cc;
 #pragma unroll
         for (int k = 0; k < PT; ++k) {
             if (k < npt && tid + k * NT < nch) {
@@ -1084,6 +1088,19 @@ static bool try_codes(const scmp_quant_args &a, dim3 grid, int G, int cpr, int n
         launch_codes<OP, 4, kGroupThreads>(a, grid, G, cpr, npt, stream);
     } else if (npt <= kMaxChunks) {
         launch_codes<OP, kMaxChunks, kGroupThreads>(a, grid, G, cpr, npt, stream);
+    } else if (OP == QOP_MUL && a.smooth_mode == SCMP_SMOOTH_NONE && chunk_mode(a) != 2 &&
+               cdiv((int64_t)G * cpr, kMidGroupThreads) <= kMidChunks) {
+        // groups of 4097 to 10240 chunks without smoothing (an attention head's P): 512
+        // threads, two workgroups per compute unit, so two groups overlap their loads and
+        // their code writes (one 1024-thread workgroup per compute unit would run the groups
+        // in lockstep rounds); the general chunk path, which takes any row layout
+        const int npt2 = (int)cdiv((int64_t)G * cpr, kMidGroupThreads);
+        if (a.code_kind == SCMP_CODE_THERMO)
+            quant_codes_kernel<QOP_MUL, kMidChunks, kMidGroupThreads, SCMP_CODE_THERMO, false,
+                               false, false><<<grid, kMidGroupThreads, 0, stream>>>(a, G, cpr, npt2);
+        else
+            quant_codes_kernel<QOP_MUL, kMidChunks, kMidGroupThreads, SCMP_CODE_Q, false, false,
+                               false><<<grid, kMidGroupThreads, 0, stream>>>(a, G, cpr, npt2);
     } else if (OP == QOP_MUL && cdiv((int64_t)G * cpr, kBigGroupThreads) <= kBigChunks) {
         launch_codes<QOP_MUL, kBigChunks, kBigGroupThreads>(
             a, grid, G, cpr, (int)cdiv((int64_t)G * cpr, kBigGroupThreads), stream);
