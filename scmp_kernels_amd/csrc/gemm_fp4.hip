@@ -22,7 +22,8 @@ static int device_cu_count() {
 // Schedule of the non-chunked FP4 kernel (TR x TC tiles, one workgroup per CU).
 struct Fp4Plan {
     int64_t tilesA, tilesB, ntiles;
-    int TR, TC;               // tile rows x columns: 256 x 256, 256 x 64 (narrow), 128 x 512
+    int TR, TC;               // tile rows x columns: 256 x 256, 256 x 64 (narrow), 128 x 512,
+                              // 256 x 224
     int nwg;                  // persistent workgroups
     bool split;               // some tiles are shared by several workgroups
     int64_t cnt_bytes, part_bytes;
@@ -46,6 +47,9 @@ static Fp4Plan fp4_plan(int64_t N, int64_t M, int64_t D, int64_t batch, int ncu,
     if (narrow_ok && M <= 64) {
         p.TR = 256;
         p.TC = 64;
+    } else if (narrow_ok && M > 192 && M <= 224) {
+        p.TR = 256;                              // 4 x 1 waves of 64 x 224
+        p.TC = 224;
     } else if (wide_fits && wide * 100 <= sq * 97) {
         p.TR = 128;
         p.TC = 512;

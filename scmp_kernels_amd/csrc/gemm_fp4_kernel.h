@@ -63,9 +63,10 @@ constexpr int kFactorFloats = 5 * 128 + 3 * 512 + 4;
 
 // Tile shapes of the persistent kernel (rows of A x rows of B per workgroup, four waves):
 // 256 x 256 (2 x 2 waves of 128 x 128), narrow 256 x 64 (4 x 1 waves of 64 x 64) for outputs
-// at most 64 wide, and wide 128 x 512 (1 x 4 waves of 128 x 128), which pads a row count
-// such as 1365 to 1408 instead of 1536.
-enum { TILE_SQUARE = 0, TILE_NARROW = 1, TILE_WIDE = 2 };
+// at most 64 wide, wide 128 x 512 (1 x 4 waves of 128 x 128), which pads a row count
+// such as 1365 to 1408 instead of 1536, and 256 x 224 (4 x 1 waves of 64 x 224) for outputs
+// 193 to 224 wide (an attention head's 197 keys: 12% less padding than 256).
+enum { TILE_SQUARE = 0, TILE_NARROW = 1, TILE_WIDE = 2, TILE_224 = 3 };
 
 // accelerator complex dies (XCDs) of an MI355X; workgroup i runs on XCD i mod 8
 constexpr int kXcds = 8;
@@ -1002,10 +1003,10 @@ static size_t fp4_tables_bytes_host(const GemmP &P) {
 // (P.ntiles when no split workspace was given: one tile each, no partial sums).
 template <int JPF, int LUTSRC, int SHAPE = TILE_SQUARE>
 static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
-    constexpr bool NARROW = SHAPE == TILE_NARROW;
-    constexpr int BA = NARROW ? 2 : 4, BB = NARROW ? 2 : 4,
-                  WA = NARROW ? 4 : SHAPE == TILE_WIDE ? 1 : 2,
-                  WB = NARROW ? 1 : SHAPE == TILE_WIDE ? 4 : 2;
+    constexpr bool NARROW = SHAPE == TILE_NARROW, T224 = SHAPE == TILE_224;
+    constexpr int BA = NARROW || T224 ? 2 : 4, BB = NARROW ? 2 : T224 ? 7 : 4,
+                  WA = NARROW || T224 ? 4 : SHAPE == TILE_WIDE ? 1 : 2,
+                  WB = NARROW || T224 ? 1 : SHAPE == TILE_WIDE ? 4 : 2;
     GemmP P = P0;
     // MFMA / LDS-read interleaving pinned for JPF = 16, 64 and >= 128; for JPF = 32 the
     // compiler's own schedule measured 9.5% faster
@@ -1126,6 +1127,7 @@ int gemm_fp4_launch_jpf(const GemmP &P, int64_t batch, bool chunked, hipStream_t
     if (P.d_class == nullptr) {
         if constexpr (JPF != 16)
             if (chunked) return launch_fp4_chunked<JPF, LUT_LDS>(P, batch, s);
+        if (P.tile_cols == 224) return launch_fp4_main<JPF, LUT_LDS, TILE_224>(P, batch, s);
         return P.tile_cols == 64 ? launch_fp4_main<JPF, LUT_LDS, TILE_NARROW>(P, batch, s)
                                  : main_kernel(Lds{});
     }

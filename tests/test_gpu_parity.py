@@ -392,6 +392,9 @@ GEMM_CASES = [
     (300, 500, 1024, 256, 256, True),
     (260, 270, 600, 128, 128, True),
     (257, 300, 777, 64, 64, False),
+    # outputs 193 to 224 wide take 256 x 224 FP4 tiles (whole, and shared at D >= 512)
+    (300, 210, 96, 256, 256, True),
+    (300, 197, 1024, 128, 128, False),
 ]
 
 
