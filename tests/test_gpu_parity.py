@@ -576,6 +576,22 @@ def test_per_head_many_large_heads(shape):
     bits_equal(y[heads], O.sc_matmul(q[heads], k[heads], "per_head"))
 
 
+@pytest.mark.parametrize("mode", ["bipolar", "unipolar"])
+@pytest.mark.parametrize("N,M,D", [(65600, 48, 96), (66000, 17, 20)])
+def test_narrow_tiles_more_than_compute_units(mode, N, M, D):
+    """Outputs at most 64 wide in more 256 x 64 tiles than compute units (whole tiles per
+    workgroup; D = 20 is three 8-d groups, the last one partial). Sampled rows of the first
+    and last tiles and random rows against the oracle."""
+    from scmp_kernels_amd import sc_matmul
+    rng = np.random.default_rng(N + M + D)
+    a = rng.standard_normal((N, D)).astype(np.float32)
+    b = rng.standard_normal((M, D)).astype(np.float32)
+    y = sc_matmul(T(a), T(b), "per_row", mode=mode)
+    rows = np.unique(np.concatenate([np.arange(0, 256, 37), np.arange(N - 300, N, 41),
+                                     rng.integers(0, N, 40)]))
+    bits_equal(y[torch.from_numpy(rows).cuda()], O.sc_matmul(a[rows], b, "per_row", mode=mode))
+
+
 def test_per_row_3d_wide_tiles_vs_oracle():
     """Batched operands whose per-batch output (300 x 500) takes 128 x 512 tiles."""
     from scmp_kernels_amd import sc_matmul
