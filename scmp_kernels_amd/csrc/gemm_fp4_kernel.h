@@ -1045,53 +1045,114 @@ static int launch_fp4_main(const GemmP &P0, int64_t batch, hipStream_t stream) {
     return SCMP_OK;
 }
 
-// Chunked launch of rows [P.row0, P.N) in TR x 128 tiles, BA x 2 blocks of 32 x 32 per wave
-// (fp32 chunk sums in registers), one workgroup per tile.
+// LDS bytes of the chunked kernel's stream tables and per-chunk scales for TR-row tiles
+template <int JPF, int LUTSRC>
+static size_t chunked_lds(const GemmP &P, int TR, size_t *tabs_out) {
+    const size_t tabs = (fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15;
+    if (tabs_out) *tabs_out = tabs;
+    return tabs + (size_t)cdiv(P.D, P.chunk) * (TR + 128) * sizeof(float);
+}
+
+// 256-row tiles only with every chunk scale in LDS: without, or with 32-interval per-d class
+// tables, the 128 x 64 wave tile spills its registers
+template <int JPF, int LUTSRC>
+static bool chunked_tall_ok(const GemmP &P) {
+    if constexpr (JPF == 32 && LUTSRC != LUT_LDS) return false;
+    return Fp4Geom<JPF>::TAB + chunked_lds<JPF, LUTSRC>(P, 256, nullptr) <= (size_t)kFp4MaxLds;
+}
+
+// Chunked launch of rows [P.row0, P.N) in TR x 128 tiles (TR = 64 BA), BA x 2 blocks of
+// 32 x 32 per wave (fp32 chunk sums in registers), one workgroup per tile.
 template <int JPF, int LUTSRC, int BA>
 static int launch_fp4_chunked_rows(const GemmP &P0, int64_t batch, hipStream_t stream) {
     constexpr int BB = 2, WA = 2, WB = 2;
-    GemmP P = P0;
-    P.tilesA = (int)cdiv(P.N - P.row0, WA * BA * 32);
-    const int64_t tilesB = cdiv(P.M, WB * BB * 32);
-    const size_t tabs = (fp4_tables_bytes_host<JPF, LUTSRC>(P) + 15) & ~(size_t)15;
-    const size_t scales = (size_t)cdiv(P.D, P.chunk) * (WA * BA * 32 + WB * BB * 32) * sizeof(float);
-    const bool slds = Fp4Geom<JPF>::TAB + tabs + scales <= (size_t)kFp4MaxLds;
-    auto kern = slds ? sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC, true>
-                     : sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC, false>;
-    const size_t lds = slds ? tabs + scales : tabs;
-    int rc = fp4_set_lds(kern, lds, Fp4Geom<JPF>::TAB);
-    if (rc != SCMP_OK) return rc;
-    kern<<<dim3((unsigned)(P.tilesA * tilesB), 1, (unsigned)batch), 64 * WA * WB, lds,
-           stream>>>(P);
-    SCMP_LAUNCH_CHECK("scmp_sc_gemm(mfma fp4, chunked)");
-    return SCMP_OK;
+    if constexpr (BA == 4 && JPF == 32 && LUTSRC != LUT_LDS) {
+        set_error("scmp_sc_gemm(mfma fp4, chunked): no 256-row tiles for these tables");
+        return SCMP_E_ARG;
+    } else {
+        GemmP P = P0;
+        P.tilesA = (int)cdiv(P.N - P.row0, WA * BA * 32);
+        const int64_t tilesB = cdiv(P.M, WB * BB * 32);
+        size_t tabs = 0;
+        const size_t with_scales = chunked_lds<JPF, LUTSRC>(P, WA * BA * 32, &tabs);
+        const bool slds = Fp4Geom<JPF>::TAB + with_scales <= (size_t)kFp4MaxLds;
+        auto kern = sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC, true>;
+        if constexpr (BA == 4) {
+            if (!chunked_tall_ok<JPF, LUTSRC>(P)) {
+                set_error("scmp_sc_gemm(mfma fp4, chunked): 256-row tiles planned without room");
+                return SCMP_E_ARG;
+            }
+        } else {
+            if (!slds) kern = sc_gemm_fp4_chunked_kernel<JPF, BA, BB, WA, WB, LUTSRC, false>;
+        }
+        const size_t lds = slds ? with_scales : tabs;
+        int rc = fp4_set_lds(kern, lds, Fp4Geom<JPF>::TAB);
+        if (rc != SCMP_OK) return rc;
+        kern<<<dim3((unsigned)(P.tilesA * tilesB), 1, (unsigned)batch), 64 * WA * WB, lds,
+               stream>>>(P);
+        SCMP_LAUNCH_CHECK("scmp_sc_gemm(mfma fp4, chunked)");
+        return SCMP_OK;
+    }
 }
 
-// Chunked: 128 x 128 tiles (each wave 64 x 64), one workgroup per tile and compute unit. The
-// inner dimension cannot be split (the fp32 chunk sums have a fixed order), so when the tiles
-// fill the compute units k + f times (0 < f < 1), the rows of the first k full rounds run as
-// 128 x 128 tiles and the rest as 64 x 128 tiles (each wave 32 x 64: half the MFMAs, three
-// quarters of the LDS reads), if that shortens the last round.
-template <int JPF, int LUTSRC>
-static int launch_fp4_chunked(const GemmP &P, int64_t batch, hipStream_t stream) {
-    const int64_t tilesB = cdiv(P.M, 128), total = cdiv(P.N, 128) * tilesB * batch;
-    const int64_t ncu = P.nwg;                            // compute units
-    const int64_t full = total / ncu;                     // complete rounds
-    if (full >= 1 && total % ncu != 0) {
-        const int64_t rows_main = full * ncu / (tilesB * batch) * 128;
-        const int64_t tail = cdiv(P.N - rows_main, 64) * tilesB * batch;
-        // time in 128 x 128 tile rounds: now full + 1; split: full + 0.75 per tail round
-        if (rows_main > 0 && rows_main < P.N && 4 * full + 3 * cdiv(tail, ncu) < 4 * (full + 1)) {
-            GemmP Pm = P;
-            Pm.N = (int)rows_main;                         // rows [0, rows_main)
-            int rc = launch_fp4_chunked_rows<JPF, LUTSRC, 2>(Pm, batch, stream);
-            if (rc != SCMP_OK) return rc;
-            GemmP Pt = P;
-            Pt.row0 = (int)rows_main;                      // rows [rows_main, N)
-            return launch_fp4_chunked_rows<JPF, LUTSRC, 1>(Pt, batch, stream);
+// Row plan of the chunked kernel: rows [0, rows_main) in main_rows x 128 tiles, the rest in
+// tail_rows x 128 tiles (a second launch; tail_rows 0: none).
+struct ChunkPlan {
+    int main_rows, tail_rows;
+    int64_t rows_main;
+};
+
+// Chunked: one workgroup per tile and compute unit. The inner dimension cannot be split (the
+// fp32 chunk sums have a fixed order), so the tiles run in rounds of one per compute unit and
+// the tile height sets both the rounds and the work of each. The kernel is bound by LDS
+// reads of the tables: a 128 x 128 tile (64 x 64 per wave) reads one 16-byte fragment per
+// lane and MFMA, a 256 x 128 tile (128 x 64 per wave: twice the MFMAs, its fp32 chunk sums
+// and accumulators fill the registers) 0.75, a 64 x 128 tile (32 x 64 per wave: half the
+// MFMAs) 1.5. Measured time of a round in tenths of a 128 x 128 round (cfg3's tiles): 256
+// rows 16, 128 rows 10, 64 rows 6. The plan is the cheapest of: all
+// rows in 128-row tiles; full rounds of 256-row (when `tall`) or 128-row tiles with the
+// remaining rows in 64- or 128-row tiles.
+static ChunkPlan chunk_plan(int64_t N, int64_t per_row_tile, int64_t ncu, bool tall) {
+    auto rounds = [&](int64_t rows, int tr) { return cdiv(cdiv(rows, tr) * per_row_tile, ncu); };
+    auto cost_of = [](int tr) { return tr == 256 ? 16 : tr == 128 ? 10 : 6; };
+    ChunkPlan best{128, 0, N};
+    int64_t best_cost = 10 * rounds(N, 128);
+    for (int mr : {256, 128}) {
+        if (mr == 256 && !tall) continue;
+        const int64_t per_round = ncu / per_row_tile;         // row tiles one round holds
+        for (int64_t k = 1; per_round > 0 && k * per_round * mr < N; ++k) {
+            const int64_t rows_main = k * per_round * mr;
+            for (int tr : {64, 128}) {
+                const int64_t c = k * cost_of(mr) + cost_of(tr) * rounds(N - rows_main, tr);
+                if (c < best_cost) {
+                    best_cost = c;
+                    best = ChunkPlan{mr, tr, rows_main};
+                }
+            }
         }
     }
+    return best;
+}
+
+template <int JPF, int LUTSRC>
+static int launch_chunked_part(const GemmP &P, int tile_rows, int64_t batch, hipStream_t stream) {
+    if (tile_rows == 256) return launch_fp4_chunked_rows<JPF, LUTSRC, 4>(P, batch, stream);
+    if (tile_rows == 64) return launch_fp4_chunked_rows<JPF, LUTSRC, 1>(P, batch, stream);
     return launch_fp4_chunked_rows<JPF, LUTSRC, 2>(P, batch, stream);
+}
+
+template <int JPF, int LUTSRC>
+static int launch_fp4_chunked(const GemmP &P, int64_t batch, hipStream_t stream) {
+    const ChunkPlan plan =
+        chunk_plan(P.N, cdiv(P.M, 128) * batch, P.nwg, chunked_tall_ok<JPF, LUTSRC>(P));
+    if (plan.tail_rows == 0) return launch_chunked_part<JPF, LUTSRC>(P, plan.main_rows, batch, stream);
+    GemmP Pm = P;
+    Pm.N = (int)plan.rows_main;                            // rows [0, rows_main)
+    int rc = launch_chunked_part<JPF, LUTSRC>(Pm, plan.main_rows, batch, stream);
+    if (rc != SCMP_OK) return rc;
+    GemmP Pt = P;
+    Pt.row0 = (int)plan.rows_main;                         // rows [rows_main, N)
+    return launch_chunked_part<JPF, LUTSRC>(Pt, plan.tail_rows, batch, stream);
 }
 
 // Stream tables: one shared table in LDS; every class table in LDS when they fit
