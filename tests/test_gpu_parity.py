@@ -758,12 +758,13 @@ def test_chunk_d_full_rounds_and_tail():
     bits_equal(y[torch.from_numpy(rows).to(y.device)], ref)
 
 
-@pytest.mark.parametrize("N,L", [(18000, 256), (22384, 256), (18000, 32)])
+@pytest.mark.parametrize("N,L", [(18000, 256), (22384, 256), (18000, 32), (18000, 64)])
 def test_chunk_d_tall_tiles_and_tail(N, L):
     """chunk_d with 256 x 128 tiles (128 x 64 per wave) in the full round: 64 of them per
     round at M = 500 cover rows 0-16383, and the rest run as 64 x 128 tiles (N = 18000) or
     128 x 128 tiles (N = 22384, whose 6000 remaining rows would take two rounds of 64-row
-    tiles). Rows at the start, around the boundary and at the end against the oracle."""
+    tiles). L = 64: one table class per d of a chunk, read from global memory. Rows at the
+    start, around the boundary and at the end against the oracle."""
     from scmp_kernels_amd import sc_matmul
     M, D = 500, 200
     rng = np.random.default_rng(N + L)
