@@ -173,6 +173,15 @@ typedef struct scmp_quant_args {
 int64_t scmp_quant_workspace_bytes(int64_t rows, int64_t cols, int64_t group, int64_t seg);
 int scmp_quantize(const scmp_quant_args *args, hipStream_t stream);
 
+/* Two independent quantizer calls, a then b, with the results of two scmp_quantize calls.
+ * Replaces the per-head path's two quantizer calls on q and k
+ * (scmp_kernels/sc/kernels.py:484-516). When both are SCMP_Q_HEAD_SYM code-only calls of
+ * dense rows (16-byte aligned, ld = code_ld = cols, no smoothing, row index or given ranges),
+ * a with THERMO codes and no column classes, b with Q codes, and each takes 5 to 16 four-column
+ * chunks per thread at 256 threads per row group, both run in one launch. Otherwise they run
+ * as two calls. */
+int scmp_quantize_pair(const scmp_quant_args *a, const scmp_quant_args *b, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------------
  * SC GEMM (replaces enable_matmul_tiled_kernel / enable_matmul_bipolar_batched_kernel /
  * enable_matmul_compact_dot_kernel, scmp_kernels/sc/kernels.py:176-332, 362-437, and the

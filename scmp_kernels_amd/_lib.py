@@ -72,7 +72,8 @@ class GemmArgs(ctypes.Structure):
 EXPORTS = [
     "scmp_abi_version", "scmp_last_error", "scmp_rng_sobol", "scmp_rng_lfsr",
     "scmp_rng_expand", "scmp_rng_prepare", "scmp_lfsr_search", "scmp_build_stream_tables",
-    "scmp_quant_workspace_bytes", "scmp_quantize", "scmp_sc_gemm", "scmp_build_bitlut",
+    "scmp_quant_workspace_bytes", "scmp_quantize", "scmp_quantize_pair", "scmp_sc_gemm",
+    "scmp_build_bitlut",
     "scmp_build_fp4_lut", "scmp_sc_gemm_workspace_bytes", "scmp_permute_code_columns",
     "scmp_sc_gemm_noalloc",
 ]
@@ -109,6 +110,8 @@ def load(path: str = LIB_PATH):
         lib.scmp_quant_workspace_bytes.argtypes = [c_i64, c_i64, c_i64, c_i64]
         lib.scmp_quant_workspace_bytes.restype = c_i64
         lib.scmp_quantize.argtypes = [ctypes.POINTER(QuantArgs), c_vp]
+        lib.scmp_quantize_pair.argtypes = [ctypes.POINTER(QuantArgs), ctypes.POINTER(QuantArgs),
+                                           c_vp]
         lib.scmp_sc_gemm.argtypes = [ctypes.POINTER(GemmArgs), c_vp]
         lib.scmp_sc_gemm_noalloc.argtypes = [ctypes.POINTER(GemmArgs), c_vp]
         lib.scmp_sc_gemm_workspace_bytes.argtypes = [ctypes.POINTER(GemmArgs)]

@@ -789,9 +789,10 @@ quant_group_kernel(scmp_quant_args a, int G, int cpr, int npt) {
 // DENSE: x rows, code rows and the group all contiguous (ld = code_ld = cols, a multiple of
 // 4, 16-byte aligned; no row index; no group across a batch): chunk k of a thread is chunk
 // tid + k * NT of the group in both buffers, so its addresses are fixed offsets.
+// blk: the group (row block) this workgroup quantizes, nblk: the groups of the call.
 template <int OP, int PT, int NT, int CODE, bool SUM, bool SMOOTH, bool DENSE>
-__global__ void __launch_bounds__(NT, NT == kMidGroupThreads ? 4 : 1)
-quant_codes_kernel(scmp_quant_args a, int G, int cpr, int npt) {
+__device__ __forceinline__ void quant_codes_body(const scmp_quant_args &a, int G, int cpr,
+                                                 int npt, int blk, int nblk) {
     __shared__ uint32_t red0[NT / 64], red1[NT / 64];
     __shared__ float rsums[SUM ? kGroupMaxRows : 1];
     __shared__ int64_t s_rowoff[kGroupMaxRows];
@@ -800,7 +801,7 @@ quant_codes_kernel(scmp_quant_args a, int G, int cpr, int npt) {
     const int sm = SMOOTH ? a.smooth_mode : SCMP_SMOOTH_NONE;
     const bool m0 = chunk_mode(a) == 0;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t r0 = (int64_t)blockIdx.x * G;
+    const int64_t r0 = (int64_t)blk * G;
     const int nr = a.rows - r0 < G ? (int)(a.rows - r0) : G;
     const int nch = nr * cpr;
     const int qmax = a.q_max;
@@ -1029,7 +1030,7 @@ quant_codes_kernel(scmp_quant_args a, int G, int cpr, int npt) {
             a.code[(b * a.code_rows + i) * a.code_ld + c] = 0;
         }
     }
-    zero_pad_share<NT>(a, cbr, blockIdx.x, gridDim.x);
+    zero_pad_share<NT>(a, cbr, blk, nblk);
     if (SUM) __syncthreads();
     for (int rr = tid; rr < nr; rr += NT) {
         const int64_t r = r0 + rr;
@@ -1038,6 +1039,27 @@ quant_codes_kernel(scmp_quant_args a, int G, int cpr, int npt) {
         if (a.zp) a.zp[r] = p.zp;
         if (SUM) a.rowsum[r] = rsums[rr];
     }
+}
+
+template <int OP, int PT, int NT, int CODE, bool SUM, bool SMOOTH, bool DENSE>
+__global__ void __launch_bounds__(NT, NT == kMidGroupThreads ? 4 : 1)
+quant_codes_kernel(scmp_quant_args a, int G, int cpr, int npt) {
+    quant_codes_body<OP, PT, NT, CODE, SUM, SMOOTH, DENSE>(a, G, cpr, npt, blockIdx.x, gridDim.x);
+}
+
+// Two calls of the same shape class in one launch (an attention call's q and k): the first
+// n1 workgroups quantize a's groups (thermometer codes), the rest b's (byte codes), so the
+// two calls' load latencies overlap instead of running one launch after the other.
+template <int OP, int PT, int NT, bool DENSE>
+__global__ void __launch_bounds__(NT, 1)
+quant_codes_pair_kernel(scmp_quant_args a, scmp_quant_args b, int n1, int G1, int cpr1,
+                        int npt1, int G2, int cpr2, int npt2) {
+    const int blk = (int)blockIdx.x;
+    if (blk < n1)
+        quant_codes_body<OP, PT, NT, SCMP_CODE_THERMO, false, false, DENSE>(a, G1, cpr1, npt1, blk, n1);
+    else
+        quant_codes_body<OP, PT, NT, SCMP_CODE_Q, false, false, DENSE>(
+            b, G2, cpr2, npt2, blk - n1, (int)gridDim.x - n1);
 }
 
 template <int OP, int PT, int NT>
@@ -1415,22 +1437,8 @@ static int quantize_groups(const scmp_quant_args &a, int64_t G, hipStream_t stre
     return SCMP_OK;
 }
 
-}  // namespace scmp
-
-using namespace scmp;
-
-extern "C" {
-
-int64_t scmp_quant_workspace_bytes(int64_t rows, int64_t cols, int64_t group, int64_t seg) {
-    int64_t G, segw, nseg;
-    unit_counts(rows, cols, group, seg, &G, &segw, &nseg);
-    int64_t nunits = cdiv(rows, G) * nseg;
-    return nunits * (int64_t)(2 * sizeof(uint32_t) + sizeof(QParams)) + 256;
-}
-
-int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
-    SCMP_REQUIRE(args != nullptr, "scmp_quantize: null args");
-    scmp_quant_args a = *args;
+// The argument checks of one quantizer call.
+static int check_quant_args(const scmp_quant_args &a) {
     SCMP_REQUIRE(a.x && a.rows > 0 && a.cols > 0 && a.ld >= a.cols,
                  "scmp_quantize: bad input shape rows=%lld cols=%lld ld=%lld",
                  (long long)a.rows, (long long)a.cols, (long long)a.ld);
@@ -1457,6 +1465,58 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
     }
     if (a.beta16 || a.beta32 || a.sign || a.xint)
         SCMP_REQUIRE(a.out_ld >= a.cols, "scmp_quantize: out_ld < cols");
+    return SCMP_OK;
+}
+
+// A call the pair launch covers: row groups of a head-symmetric quantizer into codes only,
+// dense rows (16-byte aligned, ld = code_ld = cols), no smoothing, row index or given
+// ranges, 256 threads of 5 to 16 register-held chunks each: the calls that
+// quantize_groups sends to quant_codes_kernel<QOP_MUL, kMaxChunks, kGroupThreads, ...,
+// DENSE>. G and npt as that launch takes them.
+static bool pair_eligible(const scmp_quant_args &a, int64_t *G_out, int *npt_out) {
+    int64_t G, segw, nseg;
+    unit_counts(a.rows, a.cols, a.group, a.seg, &G, &segw, &nseg);
+    if (nseg != 1 || G > kGroupMaxRows || G * a.cols > (1 << 22) || a.cols < 4) return false;
+    if (a.variant != SCMP_Q_HEAD_SYM || a.given_absmax || a.row_index ||
+        a.smooth_mode != SCMP_SMOOTH_NONE)
+        return false;
+    if (!a.code || a.beta16 || a.beta32 || a.sign || a.xint || a.rowsum || a.code_ld % 4 != 0)
+        return false;
+    if (a.code_kind == SCMP_CODE_THERMO && a.col_class != nullptr) return false;
+    const int64_t cbr = a.code_batch_rows > 0 ? a.code_batch_rows : a.rows;
+    if (cbr % G != 0 || chunk_mode(a) != 0 || a.ld != a.cols || a.code_ld != a.cols)
+        return false;
+    const int64_t cpr = cdiv(a.cols, 4), ngroups = cdiv(a.rows, G);
+    const int64_t ncu = quant_cu_count();
+    if (ngroups < 2 * ncu && G * cpr > kBigGroupThreads && G * cpr <= 4 * (int64_t)kBigGroupThreads)
+        return false;                                     // the 1024- / 512-thread launches
+    const int64_t per = cdiv(G * cpr, kGroupThreads);
+    if (per <= 4 || per > kMaxChunks) return false;
+    *G_out = G;
+    *npt_out = (int)per;
+    return true;
+}
+
+}  // namespace scmp
+
+using namespace scmp;
+
+extern "C" {
+
+int64_t scmp_quant_workspace_bytes(int64_t rows, int64_t cols, int64_t group, int64_t seg) {
+    int64_t G, segw, nseg;
+    unit_counts(rows, cols, group, seg, &G, &segw, &nseg);
+    int64_t nunits = cdiv(rows, G) * nseg;
+    return nunits * (int64_t)(2 * sizeof(uint32_t) + sizeof(QParams)) + 256;
+}
+
+int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
+    SCMP_REQUIRE(args != nullptr, "scmp_quantize: null args");
+    scmp_quant_args a = *args;
+    {
+        const int rc = check_quant_args(a);
+        if (rc != SCMP_OK) return rc;
+    }
     int64_t G, segw, nseg;
     unit_counts(a.rows, a.cols, a.group, a.seg, &G, &segw, &nseg);
     if (a.variant == SCMP_Q_TENSOR_SYM || a.variant == SCMP_Q_TENSOR_ASYM ||
@@ -1510,6 +1570,30 @@ int scmp_quantize(const scmp_quant_args *args, hipStream_t stream) {
         tensor_out_kernel<<<1, 1, 0, stream>>>(prm, a.scale64, a.zp64);
         SCMP_LAUNCH_CHECK("scmp_quantize/tensor_out");
     }
+    return SCMP_OK;
+}
+
+int scmp_quantize_pair(const scmp_quant_args *a, const scmp_quant_args *b, hipStream_t stream) {
+    SCMP_REQUIRE(a != nullptr && b != nullptr, "scmp_quantize_pair: null args");
+    int64_t G1 = 0, G2 = 0;
+    int npt1 = 0, npt2 = 0;
+    const bool fuse = a->code_kind == SCMP_CODE_THERMO && b->code_kind == SCMP_CODE_Q &&
+                      pair_eligible(*a, &G1, &npt1) && pair_eligible(*b, &G2, &npt2);
+    if (!fuse) {
+        const int rc = scmp_quantize(a, stream);
+        return rc != SCMP_OK ? rc : scmp_quantize(b, stream);
+    }
+    int rc = check_quant_args(*a);
+    if (rc != SCMP_OK) return rc;
+    rc = check_quant_args(*b);
+    if (rc != SCMP_OK) return rc;
+    const int64_t n1 = cdiv(a->rows, G1), n2 = cdiv(b->rows, G2);
+    SCMP_REQUIRE(n1 + n2 <= (int64_t)INT32_MAX, "scmp_quantize_pair: too many row groups");
+    quant_codes_pair_kernel<QOP_MUL, kMaxChunks, kGroupThreads, true>
+        <<<(unsigned)(n1 + n2), kGroupThreads, 0, stream>>>(
+            *a, *b, (int)n1, (int)G1, (int)cdiv(a->cols, 4), npt1, (int)G2,
+            (int)cdiv(b->cols, 4), npt2);
+    SCMP_LAUNCH_CHECK("scmp_quantize_pair");
     return SCMP_OK;
 }
 

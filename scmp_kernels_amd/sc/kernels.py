@@ -103,17 +103,14 @@ def _workspace(rows, cols, group, seg, device):
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
-def quantize(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, *, group: int = 1,
-             seg: int = 0, smooth: Optional[torch.Tensor] = None, smooth_mode: int = 0,
-             code: Optional[torch.Tensor] = None, code_kind: int = 0,
-             code_batch_rows: int = 0, jtab=None, col_class=None, beta16=None, beta32=None,
-             beta_formula: int = 0, sign=None, xint=None, scale=None, scale64=None, inv=None,
-             zp=None, zp64=None, rowsum=None, host_inv: float = 0.0, host_zp: float = 0.0,
-             row_index=None, given_absmax=None):
-    """One scmp_quantize call on the current stream; outputs are written in place.
-    row_index (int64 device tensor): quantize rows x[row_index] in that order.
-    given_absmax (float32 device tensor, one value per row group): the groups' max|x| from
-    the caller instead of the reduction (symmetric variants)."""
+def _quant_args(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, *, group: int = 1,
+                seg: int = 0, smooth: Optional[torch.Tensor] = None, smooth_mode: int = 0,
+                code: Optional[torch.Tensor] = None, code_kind: int = 0,
+                code_batch_rows: int = 0, jtab=None, col_class=None, beta16=None, beta32=None,
+                beta_formula: int = 0, sign=None, xint=None, scale=None, scale64=None,
+                inv=None, zp=None, zp64=None, rowsum=None, host_inv: float = 0.0,
+                host_zp: float = 0.0, row_index=None, given_absmax=None):
+    """The scmp_quant_args of one quantizer call, its workspace and its observer info."""
     x = _rows2d(x)
     rows, cols = x.shape
     if row_index is not None:
@@ -138,15 +135,47 @@ def quantize(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, *, grou
     a.workspace = ws.data_ptr()
     a.row_index = _lib.ptr(row_index)
     a.given_absmax = _lib.ptr(given_absmax)
-    info = None
+    info = {"rows": rows, "cols": cols, "in_bytes": 4 * rows * cols,
+            "code_bytes": 0 if code is None else code.numel(), "variant": variant}
+    return a, ws, info, x.device
+
+
+def quantize(x: torch.Tensor, variant: int, q_max: int, rng_levels: int, **kw):
+    """One scmp_quantize call on the current stream; outputs are written in place (keywords
+    as _quant_args). row_index (int64 device tensor): quantize rows x[row_index] in that
+    order. given_absmax (float32 device tensor, one value per row group): the groups' max|x|
+    from the caller instead of the reduction (symmetric variants)."""
+    a, ws, info, dev = _quant_args(x, variant, q_max, rng_levels, **kw)
     if launch_observer is not None:
-        info = {"rows": rows, "cols": cols, "in_bytes": 4 * rows * cols,
-                "code_bytes": 0 if code is None else code.numel(), "variant": variant}
         _observe("pre", "quantize", info)
-    _lib.check(_lib.load().scmp_quantize(a, _lib.stream_of(x.device)), "scmp_quantize")
-    if info is not None:
+    _lib.check(_lib.load().scmp_quantize(a, _lib.stream_of(dev)), "scmp_quantize")
+    if launch_observer is not None:
         _observe("post", "quantize", info)
     return ws  # keep the workspace alive until the stream has consumed it
+
+
+def quantize_pair(first: tuple, second: tuple):
+    """Two independent quantizer calls, each (x, variant, q_max, rng_levels, keywords), as
+    one scmp_quantize_pair call: one launch when both are head-symmetric code-only calls of
+    the dense shape (the first with thermometer codes, the second with byte codes), else
+    the two calls in order (as two quantize calls when a row is not whole 4-column chunks,
+    which the single launch never takes). Returns both workspaces."""
+    if first[0].shape[-1] % 4 or second[0].shape[-1] % 4:
+        return quantize(*first[:4], **first[4]), quantize(*second[:4], **second[4])
+    a, ws1, i1, dev = _quant_args(*first[:4], **first[4])
+    b, ws2, i2, _ = _quant_args(*second[:4], **second[4])
+    info = None
+    if launch_observer is not None:
+        info = dict(i1)
+        if i1["cols"] == i2["cols"]:
+            info["rows"] = i1["rows"] + i2["rows"]
+        info["in_bytes"] = i1["in_bytes"] + i2["in_bytes"]
+        info["code_bytes"] = i1["code_bytes"] + i2["code_bytes"]
+        _observe("pre", "quantize", info)
+    _lib.check(_lib.load().scmp_quantize_pair(a, b, _lib.stream_of(dev)), "scmp_quantize_pair")
+    if info is not None:
+        _observe("post", "quantize", info)
+    return ws1, ws2
 
 
 def _gemm_impl() -> Optional[int]:
@@ -703,12 +732,15 @@ def _sc_matmul_per_head_bipolar(q_flat, k_flat, q_maxs=None, q_mins=None, k_maxs
     sk = torch.empty(BH * M, dtype=torch.float32, device=dev)
     s_a, m_a = _smooth_args(smooth_scales, "a")
     s_b, m_b = _smooth_args(smooth_scales, "b")
-    w1 = quantize(q_flat.reshape(BH * N, D), _lib.Q_HEAD_SYM, Q, R, group=N, smooth=s_a,
-                  smooth_mode=m_a, code=ca, code_kind=_lib.CODE_THERMO, code_batch_rows=N,
-                  jtab=tabs.jtab, col_class=tabs.d_class, scale=sq, given_absmax=gq)
-    w2 = quantize(k_flat.reshape(BH * M, D), _lib.Q_HEAD_SYM, Q, R, group=M, smooth=s_b,
-                  smooth_mode=m_b, code=cb, code_kind=_lib.CODE_Q, code_batch_rows=M, scale=sk,
-                  given_absmax=gk)
+    # both quantizer calls in one launch when their shapes allow (the library checks)
+    w1, w2 = quantize_pair(
+        (q_flat.reshape(BH * N, D), _lib.Q_HEAD_SYM, Q, R,
+         dict(group=N, smooth=s_a, smooth_mode=m_a, code=ca, code_kind=_lib.CODE_THERMO,
+              code_batch_rows=N, jtab=tabs.jtab, col_class=tabs.d_class, scale=sq,
+              given_absmax=gq)),
+        (k_flat.reshape(BH * M, D), _lib.Q_HEAD_SYM, Q, R,
+         dict(group=M, smooth=s_b, smooth_mode=m_b, code=cb, code_kind=_lib.CODE_Q,
+              code_batch_rows=M, scale=sk, given_absmax=gk)))
     # out_scale = scale_q * scale_k (kernels.py:550), fp32: the kernel multiplies the
     # head's first row scales (every row of a head has the head's scale)
     y = torch.empty((BH, N, M), dtype=torch.float32, device=dev)

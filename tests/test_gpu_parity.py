@@ -561,6 +561,41 @@ def test_per_head_vs_oracle(shape):
     bits_equal(y, O.sc_matmul(q, k, "per_head"))
 
 
+@pytest.mark.parametrize("D", [64, 66])
+def test_quantize_pair_equals_two_calls(D):
+    """scmp_quantize_pair against two scmp_quantize calls, bitwise (codes with their padding
+    rows, per-row scales): per-head q (thermometer codes) and k (byte codes) of 600 heads of
+    197 rows; D = 64 runs as one launch, D = 66 (rows not 16-byte aligned) as two calls."""
+    from scmp_kernels_amd import _lib
+    from scmp_kernels_amd.sc import kernels as K
+    BH, N = 600, 197
+    rng = np.random.default_rng(D)
+    q = T(rng.standard_normal((BH * N, D)).astype(np.float32))
+    k = T(rng.standard_normal((BH * N, D)).astype(np.float32) * 3)
+    tabs = K._get_tables(None, 8, 256, 128, True, D, _dev())
+    outs = []
+    for paired in (False, True):
+        ca, cb = K._codes(N, D, _dev(), batch=BH), K._codes(N, D, _dev(), batch=BH)
+        ca.fill_(0x5A)
+        cb.fill_(0xA5)
+        sq = torch.full((BH * N,), -1.0, device=_dev())
+        sk = torch.full((BH * N,), -1.0, device=_dev())
+        first = (q, _lib.Q_HEAD_SYM, 127, 128,
+                 dict(group=N, code=ca, code_kind=_lib.CODE_THERMO, code_batch_rows=N,
+                      jtab=tabs.jtab, col_class=tabs.d_class, scale=sq))
+        second = (k, _lib.Q_HEAD_SYM, 127, 128,
+                  dict(group=N, code=cb, code_kind=_lib.CODE_Q, code_batch_rows=N, scale=sk))
+        if paired:
+            ws = K.quantize_pair(first, second)
+        else:
+            ws = (K.quantize(*first[:4], **first[4]), K.quantize(*second[:4], **second[4]))
+        torch.cuda.synchronize()
+        outs.append([t.cpu().numpy() for t in (ca, cb, sq, sk)])
+        del ws
+    for x, y in zip(*outs):
+        np.testing.assert_array_equal(x.view(np.uint8), y.view(np.uint8))
+
+
 @pytest.mark.parametrize("shape", [(600, 197, 197, 64), (300, 96, 384, 96), (260, 40, 900, 40)])
 def test_per_head_many_large_heads(shape):
     """More heads than compute units, heads of 64 to 155 KB of fp32 (P-like 197 x 197;
